@@ -1,0 +1,367 @@
+"""Benchmark of the MI355X GDN state codec hot path.
+
+Headline workload: one step = quantize + dequantize of a
+[30 layers, 256 seqs, 32 heads, 128, 128] fp32 GDN state (16.1 GB, layout
+[L,B,H,K,V]).  Also measured each run: the decode encoded projection at B=256
+(config 3) and the chunked projection 64 x T=64 x 32 heads (config 4), both
+rotating over 5 distinct state copies so the 256 MB Infinity Cache cannot hold
+the working set.  Kernel durations come from HIP events recorded on the stream
+the kernels are launched on (torch's current stream).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--pool]
+
+Prints one JSON line (rank 0).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "gdn-state-codec_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "codec GB/s + % HBM peak; encoded-proj µs/decode step at B=256"
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+C2_SHAPE = (30, 256, 32, 128, 128)
+C2_TILES = 30 * 256 * 32
+C2_ELEMENTS = C2_TILES * 128 * 128
+# quantize: fp32 in + int8 codes + fp32 smoothing & scales out; dequantize mirrors it.
+C2_BYTES = C2_ELEMENTS * 4 + C2_ELEMENTS + C2_TILES * 2 * 128 * 4  # 20,384,317,440
+C3_BYTES = 256 * 32 * 128 * 128 + 2 * 256 * 32 * 128 * 4 + 256 * 16 * 128 * 2 + 256 * 32 * 128 * 4
+C4_BYTES = 64 * 32 * 128 * 128 + 2 * 64 * 32 * 128 * 4 + 64 * 64 * 32 * 128 * 2 + 64 * 64 * 32 * 128 * 4
+C4_FLOPS = 2 * 64 * 64 * 32 * 128 * 128
+ROTATIONS = 5
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _events_ms(pairs) -> list[float]:
+    import torch
+
+    torch.cuda.synchronize()
+    return [start.elapsed_time(end) for start, end in pairs]
+
+
+def bench_codec(steps: int, warmup: int):
+    import torch
+
+    from gdn_state_codec import codec
+
+    dev = torch.device("cuda:0")
+    _log(f"config 2: allocating {C2_SHAPE} fp32 state")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20261201)
+    state = torch.randn(C2_SHAPE, generator=gen, device=dev, dtype=torch.float32)
+    state.mul_(0.05)
+    codes = torch.empty(C2_SHAPE, dtype=torch.int8, device=dev)
+    smoothing = torch.empty(C2_SHAPE[:-1], dtype=torch.float32, device=dev)
+    scales = torch.empty(C2_SHAPE[:-1], dtype=torch.float32, device=dev)
+    dense = torch.empty_like(state)
+    layout = codec.LAYOUT_KEY_VALUE
+
+    def step():
+        codec.encode(state, layout, codes, smoothing, scales)
+        codec.decode(codes, smoothing, scales, layout, out=dense)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    enc, dec = [], []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        e0.record()
+        codec.encode(state, layout, codes, smoothing, scales)
+        e1.record()
+        codec.decode(codes, smoothing, scales, layout, out=dense)
+        e2.record()
+        enc.append((e0, e1))
+        dec.append((e1, e2))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    enc_ms = sum(_events_ms(enc)) / steps
+    dec_ms = sum(_events_ms(dec)) / steps
+    _log(f"config 2: quantize {enc_ms:.3f} ms, dequantize {dec_ms:.3f} ms")
+    return state, codes, smoothing, scales, dense, enc_ms, dec_ms, wall * 1e3 / steps
+
+
+def bench_hbm_copy():
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(1 << 30, dtype=torch.int32, device=dev)  # 4 GiB
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    pairs = []
+    for _ in range(5):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(src)
+        b.record()
+        pairs.append((a, b))
+    ms = min(_events_ms(pairs))
+    del src, dst
+    return 2 * 4 * (1 << 30) / (ms * 1e-3) / 1e9
+
+
+def _c1_style_state(shape, gen, dev):
+    import torch
+
+    x = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).mul_(0.05)
+    mask = torch.rand(shape, generator=gen, device=dev) < 0.001
+    signs = torch.where(torch.rand(shape, generator=gen, device=dev) < 0.5, -2.0, 2.0)
+    return torch.where(mask, signs, x)
+
+
+def bench_decode_projection(steps: int, warmup: int):
+    import torch
+
+    from gdn_state_codec import codec
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    sets = []
+    for _ in range(ROTATIONS):
+        x = _c1_style_state((256, 32, 128, 128), gen, dev)
+        c, s, sc = codec.encode(x, codec.LAYOUT_VALUE_KEY)
+        q = torch.randn((256, 16, 128), generator=gen, device=dev)
+        q = (q / q.norm(dim=-1, keepdim=True)).to(torch.bfloat16)
+        out = torch.empty((256, 32, 128), dtype=torch.float32, device=dev)
+        sets.append((c, s, sc, q, out))
+        del x
+    for i in range(warmup * ROTATIONS):
+        c, s, sc, q, out = sets[i % ROTATIONS]
+        codec.project_decode(c, s, sc, q, 1.0, codec.LAYOUT_VALUE_KEY, out)
+    pairs = []
+    n = max(steps, 4) * ROTATIONS
+    for i in range(n):
+        c, s, sc, q, out = sets[i % ROTATIONS]
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        codec.project_decode(c, s, sc, q, 1.0, codec.LAYOUT_VALUE_KEY, out)
+        b.record()
+        pairs.append((a, b))
+    us = sum(_events_ms(pairs)) / n * 1e3
+    _log(f"config 3: decode projection {us:.2f} us/step")
+    return us
+
+
+def bench_chunked_projection(steps: int, warmup: int):
+    import torch
+
+    from gdn_state_codec import codec
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    sets = []
+    for _ in range(ROTATIONS):
+        x = _c1_style_state((64, 32, 128, 128), gen, dev)
+        c, s, sc = codec.encode(x, codec.LAYOUT_VALUE_KEY)
+        q = torch.randn((64, 64, 32, 128), generator=gen, device=dev).to(torch.bfloat16)
+        out = torch.empty((64, 64, 32, 128), dtype=torch.float32, device=dev)
+        sets.append((c, s, sc, q, out))
+        del x
+    for i in range(warmup * ROTATIONS):
+        c, s, sc, q, out = sets[i % ROTATIONS]
+        codec.project_chunked(c, s, sc, q, 1.0, codec.LAYOUT_VALUE_KEY, out)
+    pairs = []
+    n = max(steps, 4) * ROTATIONS
+    for i in range(n):
+        c, s, sc, q, out = sets[i % ROTATIONS]
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        codec.project_chunked(c, s, sc, q, 1.0, codec.LAYOUT_VALUE_KEY, out)
+        b.record()
+        pairs.append((a, b))
+    us = sum(_events_ms(pairs)) / n * 1e3
+    _log(f"config 4: chunked projection {us:.2f} us/step")
+    return us
+
+
+def bench_pool(steps: int, warmup: int):
+    """Config 5 with a bf16 pool (64.4 GB): gather-encode and decode-scatter."""
+    import torch
+
+    from gdn_state_codec import codec
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    layers, slots, heads, batch = 30, 2048, 32, 512
+    pool = torch.empty((layers, slots, heads, 128, 128), dtype=torch.bfloat16, device=dev)
+    for layer in range(layers):
+        t = torch.distributions.StudentT(torch.tensor(3.0, device=dev))
+        pool[layer] = (t.sample((slots, heads, 128, 128)) * 0.05).to(torch.bfloat16)
+    zero = torch.rand((layers, slots, heads), generator=gen, device=dev) < 0.02
+    pool[zero] = 0
+    perm = torch.randperm(slots, generator=gen, device=dev)[:batch].to(torch.int32)
+    pad = torch.randperm(batch, generator=gen, device=dev)[:26]
+    perm[pad] = -1
+    codes, s, sc = codec.pool_encode(pool, perm)
+    for _ in range(warmup):
+        codec.pool_encode(pool, perm, codec.LAYOUT_KEY_VALUE, codes, s, sc)
+        codec.pool_decode(codes, s, sc, perm, pool)
+    enc, dec = [], []
+    for _ in range(steps):
+        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        e0.record()
+        codec.pool_encode(pool, perm, codec.LAYOUT_KEY_VALUE, codes, s, sc)
+        e1.record()
+        codec.pool_decode(codes, s, sc, perm, pool)
+        e2.record()
+        enc.append((e0, e1))
+        dec.append((e1, e2))
+    enc_ms = sum(_events_ms(enc)) / steps
+    dec_ms = sum(_events_ms(dec)) / steps
+    valid = batch - 26
+    per_head = 128 * 128 * 2 + 128 * 128 + 2 * 128 * 4
+    nbytes = valid * layers * heads * per_head
+    del pool, codes
+    return {"encode_ms": enc_ms, "decode_ms": dec_ms,
+            "encode_GBps": nbytes / (enc_ms * 1e-3) / 1e9,
+            "decode_GBps": nbytes / (dec_ms * 1e-3) / 1e9,
+            "bytes_per_direction": nbytes, "pool_dtype": "bf16"}
+
+
+def cpu_baseline(state, codes, smoothing, scales, target_seconds: float = 10.0):
+    """The reference's own C++ CPU path (oracle/_ref) when it is present,
+    else the C restatement, on one thread, over a bounded sample of heads of the
+    same config-2 state; also checks the GPU codes of the sample bit-exactly."""
+    import numpy as np
+
+    import oracle
+
+    kind = "reference" if oracle.ref_available() else "port"
+    flat = state.view(-1, 128, 128)
+
+    def run(n):
+        x = flat[:n].cpu().numpy()
+        t0 = time.perf_counter()
+        if kind == "reference":
+            c, s, sc = oracle.ref_quantize_heads(x)
+            oracle.ref_dequantize_heads(c, s, sc)
+        else:
+            c, s, sc = oracle.encode_heads(x, oracle.LAYOUT_KEY_VALUE, threads=1)
+            oracle.decode_heads(c, s, sc, oracle.LAYOUT_KEY_VALUE, threads=1)
+        return time.perf_counter() - t0, c, s, sc
+
+    probe, _, _, _ = run(64)
+    n = int(min(max(64, target_seconds / max(probe, 1e-6) * 64), 16384))
+    seconds, c, s, sc = run(n)
+    parity = (codes.view(-1, 128, 128)[:n].cpu().numpy().tobytes() == c.tobytes()
+              and smoothing.view(-1, 128)[:n].cpu().numpy().tobytes() == s.tobytes()
+              and scales.view(-1, 128)[:n].cpu().numpy().tobytes() == sc.tobytes())
+    per_head = 2 * (128 * 128 * 5 + 2 * 128 * 4)  # quantize + dequantize bytes
+    value = n * per_head / seconds / 1e9
+    _log(f"cpu baseline ({kind}): {n} heads in {seconds:.1f} s -> {value:.3f} GB/s, parity={parity}")
+    return {"value": value, "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{n} heads (first {n} of layer 0) of the config-2 state, "
+                      "quantize+dequantize, 1 thread", "seconds": seconds,
+            "gpu_codes_bit_exact_on_sample": bool(parity)}
+
+
+def _traffic():
+    path = ROOT / "profiles" / "encode_c2_traffic.json"
+    if not path.is_file():
+        return None
+    try:
+        return json.loads(path.read_text()).get("bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--pool", action="store_true", help="also run config 5 (bf16 pool)")
+    parser.add_argument("--only-codec", action="store_true", help="config 2 only (profiling)")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(every head tile is independent; see DESIGN.md for the sharding plan).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    torch.cuda.init()
+    state, codes, smoothing, scales, dense, enc_ms, dec_ms, wall_ms = bench_codec(
+        args.steps, args.warmup)
+    step_ms = enc_ms + dec_ms
+    value = 2 * C2_BYTES / (step_ms * 1e-3) / 1e9
+    enc_gbps = C2_BYTES / (enc_ms * 1e-3) / 1e9
+    dec_gbps = C2_BYTES / (dec_ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu else cpu_baseline(state, codes, smoothing, scales)
+    del state, dense, codes, smoothing, scales
+    torch.cuda.empty_cache()
+    extra = {}
+    if not args.only_codec:
+        extra["hbm_copy_GBps"] = bench_hbm_copy()
+        dec_us = bench_decode_projection(args.steps, args.warmup)
+        chunk_us = bench_chunked_projection(args.steps, args.warmup)
+        extra["decode_projection"] = {
+            "workload": "config 3: B=256, 32 value heads (GQA from 16), int8 [256,32,128,128]",
+            "us_per_step": dec_us, "GBps": C3_BYTES / (dec_us * 1e-6) / 1e9,
+            "hbm_frac": C3_BYTES / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+            "bytes_per_step": C3_BYTES, "rotated_state_copies": ROTATIONS}
+        extra["chunked_projection"] = {
+            "workload": "config 4: 64 seqs x T=64 x 32 heads, bf16 MFMA",
+            "us_per_step": chunk_us, "GBps": C4_BYTES / (chunk_us * 1e-6) / 1e9,
+            "hbm_frac": C4_BYTES / (chunk_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+            "TFLOPs": C4_FLOPS / (chunk_us * 1e-6) / 1e12,
+            "mfma_frac_of_useful_flops": C4_FLOPS / (chunk_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "bytes_per_step": C4_BYTES, "rotated_state_copies": ROTATIONS}
+    if args.pool:
+        extra["pool_codec"] = bench_pool(max(args.steps // 4, 2), 1)
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_ms,
+        "wall_ms_per_step": wall_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (torch.randn * 0.05, seeded, generated on the GPU)",
+        "config": {"workload": "config 2: batched quantize + dequantize of a [30,256,32,128,128] "
+                               "fp32 GDN state, layout [L,B,H,K,V]",
+                   "tiles": C2_TILES, "bytes_per_direction": C2_BYTES},
+        "quantize": {"ms": enc_ms, "GBps": enc_gbps, "hbm_frac": enc_gbps / HBM_PEAK_GBPS},
+        "dequantize": {"ms": dec_ms, "GBps": dec_gbps, "hbm_frac": dec_gbps / HBM_PEAK_GBPS},
+        "roofline": {"kernel": "encode_kernel (quantize)", "bound": "hbm",
+                     "achieved": enc_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": enc_gbps / HBM_PEAK_GBPS, "traffic": _traffic(),
+                     "algorithmic_bytes_per_launch": C2_BYTES},
+        "cpu_baseline": cpu,
+        **extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

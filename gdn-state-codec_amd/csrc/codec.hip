@@ -1,0 +1,659 @@
+// Quant-only int8 codec of GDN recurrent-state head tiles on gfx950.
+//
+// Numerics follow the reference's portable C++ quant stage bit for bit
+// (native/src/gdn_state_codec_state_capsule.cpp:190-226 encode, :229-251
+// decode):
+//   s[k]     = sqrtf(max((float)(sum_v |r[k][v]| in double, in v order) / 128, 1e-8))
+//   m[k][v]  = r[k][v] / s[k]
+//   scale[v] = max_k |m[k][v]|
+//   code     = scale == 0 ? 0 : lround(m / scale * 127)      (clamped to +-127)
+//   dense    = ((s[k] * code) / 127) * scale[v] (+ sum_r ck[k][r] * cv[v][r])
+//
+// One workgroup of 256 threads (4 wavefronts) owns one 128x128 tile.  Thread t
+// holds rows 8j + t/32 (j = 0..15) and the four consecutive columns
+// 4*(t%32)..+3 of each, so every load instruction of a wavefront reads 1 KiB of
+// contiguous HBM and every code store writes 256 contiguous bytes.  "Row" and
+// "column" are the tile's memory-major and minor axes; which of them is the key
+// axis depends on the layout.
+//
+// The smoothing sum is order-dependent only when some partial sum needs more
+// than 53 bits.  All terms are non-negative multiples of 2^(e_min-23) (e_min:
+// exponent of the smallest non-zero |r| of the tile, at least -126), so when
+// the largest key sum T satisfies T < 2^(e_min+29) every partial sum, in any
+// order, is exact and equals the reference's sequential double sum.  The
+// kernel sums with a lane tree, checks that bound per tile, and otherwise
+// recomputes the 128 key sums serially in the reference's order.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "codec_math.h"
+#include "launch.h"
+
+namespace gdn {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerThread = 16;
+
+// Encode modes.
+constexpr int kModeEncode = 0;         // smoothing + scales + codes
+constexpr int kModeSmoothingOnly = 1;  // smoothing only
+constexpr int kModeGivenSmoothing = 2; // scales + codes from caller's smoothing
+
+// Work-item -> tile mapping.  Without slot ids item i is tile i on both sides.
+// With slot ids, item i = (layer * batch + entry) * heads + head indexes the
+// compact encoded side and the pool side is tile
+// (layer * slots + slot_ids[entry]) * heads + head; entries whose slot id is
+// negative (padding) or not below `slots` are skipped.
+struct TileMap {
+  const int32_t* slot_ids;
+  uint32_t batch;
+  uint32_t heads;
+  uint32_t slots;
+};
+
+__device__ __forceinline__ bool pool_entry(const TileMap& map, uint64_t item,
+                                           uint64_t* entry) {
+  if (map.slot_ids == nullptr) {
+    *entry = item;
+    return true;
+  }
+  const uint64_t head = item % map.heads;
+  const uint64_t rest = item / map.heads;
+  const uint64_t batch_entry = rest % map.batch;
+  const uint64_t layer = rest / map.batch;
+  const int32_t slot = map.slot_ids[batch_entry];
+  if (slot < 0 || static_cast<uint32_t>(slot) >= map.slots) return false;
+  *entry = (layer * map.slots + static_cast<uint64_t>(slot)) * map.heads + head;
+  return true;
+}
+
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, float (&v)[4]);
+
+template <>
+__device__ __forceinline__ void load4<float>(const float* p, float (&v)[4]) {
+  const float4 q = *reinterpret_cast<const float4*>(p);
+  v[0] = q.x;
+  v[1] = q.y;
+  v[2] = q.z;
+  v[3] = q.w;
+}
+
+template <>
+__device__ __forceinline__ void load4<uint16_t>(const uint16_t* p,
+                                                float (&v)[4]) {
+  const uint2 q = *reinterpret_cast<const uint2*>(p);
+  v[0] = bf16_to_float(static_cast<uint16_t>(q.x & 0xFFFFu));
+  v[1] = bf16_to_float(static_cast<uint16_t>(q.x >> 16));
+  v[2] = bf16_to_float(static_cast<uint16_t>(q.y & 0xFFFFu));
+  v[3] = bf16_to_float(static_cast<uint16_t>(q.y >> 16));
+}
+
+__device__ __forceinline__ float load1(const float* p) { return *p; }
+__device__ __forceinline__ float load1(const uint16_t* p) {
+  return bf16_to_float(*p);
+}
+
+__device__ __forceinline__ void store4(float* p, const float (&v)[4]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ void store4(uint16_t* p, const float (&v)[4]) {
+  uint2 q;
+  q.x = static_cast<uint32_t>(float_to_bf16(v[0])) |
+        (static_cast<uint32_t>(float_to_bf16(v[1])) << 16);
+  q.y = static_cast<uint32_t>(float_to_bf16(v[2])) |
+        (static_cast<uint32_t>(float_to_bf16(v[3])) << 16);
+  *reinterpret_cast<uint2*>(p) = q;
+}
+
+// One reduce-scatter step over lane pairs (lane, lane ^ mask) for an array of
+// 2H partials: the lane whose `mask` bit is clear keeps the low half, its
+// partner the high half, and each adds the partner's copy of the half it keeps.
+template <int H, typename T, typename Op>
+__device__ __forceinline__ void reduce_scatter_step(T* p, bool upper, int mask,
+                                                    Op op) {
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const T send = upper ? p[i] : p[i + H];
+    const T keep = upper ? p[i + H] : p[i];
+    p[i] = op(keep, __shfl_xor(send, mask));
+  }
+}
+
+// Reduces 16 per-row partials over the 32 lanes of a half-wavefront.  Lane c
+// (c = lane % 32) ends holding, in p[0], the total of row (c >> 1) & 15; lanes
+// c and c ^ 1 hold the same value.
+template <typename T, typename Op>
+__device__ __forceinline__ void reduce_rows_over_half_wave(T (&p)[16], int c,
+                                                           Op op) {
+  reduce_scatter_step<8>(p, (c & 16) != 0, 16, op);
+  reduce_scatter_step<4>(p, (c & 8) != 0, 8, op);
+  reduce_scatter_step<2>(p, (c & 4) != 0, 4, op);
+  reduce_scatter_step<1>(p, (c & 2) != 0, 2, op);
+  p[0] = op(p[0], __shfl_xor(p[0], 1));
+}
+
+struct AddOp {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T a, T b) const {
+    return a + b;
+  }
+};
+struct MaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const {
+    return fmaxf(a, b);
+  }
+};
+
+// Exponent that bounds the granularity of a non-negative float: every float
+// >= 2^e is a multiple of 2^(e-23), and every float is a multiple of 2^-149.
+__device__ __forceinline__ int granularity_exponent(float value) {
+  const int biased = static_cast<int>((__float_as_uint(value) >> 23) & 0xFFu);
+  return biased == 0 ? -126 : biased - 127;
+}
+
+// The reference's sequential double sum of |r| along one key
+// (state_capsule.cpp:193-197), read straight from the tile.
+template <uint32_t kLayout, typename In>
+__device__ double serial_key_sum(const In* tile, int key) {
+  double sum = 0.0;
+  if constexpr (kLayout == kKeyValue) {
+    const In* row = tile + key * kDim;
+    for (int value = 0; value < kDim; ++value) sum += fabsf(load1(row + value));
+  } else {
+    for (int value = 0; value < kDim; ++value) {
+      sum += fabsf(load1(tile + value * kDim + key));
+    }
+  }
+  return sum;
+}
+
+template <uint32_t kLayout, typename In, int kMode>
+__global__ __launch_bounds__(kThreads) void encode_kernel(
+    const In* __restrict__ source, int8_t* __restrict__ codes,
+    float* __restrict__ smoothing, float* __restrict__ scales,
+    const float* __restrict__ given_smoothing, TileMap map) {
+  __shared__ double key_sum[kDim];
+  __shared__ double sum_part[4][kDim];
+  __shared__ float max_part[4][kDim];
+  __shared__ float s_shared[kDim];
+  __shared__ float s_inverse[kDim];
+  __shared__ float scale_shared[kDim];
+  __shared__ float scale_inverse[kDim];
+  __shared__ float min_part[4];
+  __shared__ double tmax_part[4];
+
+  const uint64_t item = blockIdx.x;
+  uint64_t entry;
+  if (!pool_entry(map, item, &entry)) return;  // uniform over the workgroup
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int group = t >> 5;  // row offset within each group of 8 rows
+  const int c4 = t & 31;     // column quad
+  const In* tile = source + entry * kTile;
+
+  float x[kRowsPerThread][4];
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    load4(tile + (8 * j + group) * kDim + 4 * c4, x[j]);
+  }
+
+  bool fast_divide = false;
+  if constexpr (kMode != kModeGivenSmoothing) {
+    // ---- smoothing: per-key double sums of |r| ------------------------------
+    float min_abs = fabsf(x[0][0]);
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) min_abs = fminf(min_abs, fabsf(x[j][i]));
+    }
+    if constexpr (kLayout == kKeyValue) {
+      double p[kRowsPerThread];
+#pragma unroll
+      for (int j = 0; j < kRowsPerThread; ++j) {
+        p[j] = (static_cast<double>(fabsf(x[j][0])) +
+                static_cast<double>(fabsf(x[j][1]))) +
+               (static_cast<double>(fabsf(x[j][2])) +
+                static_cast<double>(fabsf(x[j][3])));
+      }
+      reduce_rows_over_half_wave(p, c4, AddOp{});
+      if ((c4 & 1) == 0) key_sum[8 * ((c4 >> 1) & 15) + group] = p[0];
+    } else {
+      double p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        double acc = 0.0;
+#pragma unroll
+        for (int j = 0; j < kRowsPerThread; ++j) {
+          acc += static_cast<double>(fabsf(x[j][i]));
+        }
+        p[i] = acc + __shfl_xor(acc, 32);
+      }
+      if (lane < 32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sum_part[wave][4 * c4 + i] = p[i];
+      }
+      __syncthreads();
+      if (t < kDim) {
+        key_sum[t] = (sum_part[0][t] + sum_part[1][t]) +
+                     (sum_part[2][t] + sum_part[3][t]);
+      }
+    }
+    __syncthreads();
+
+    // Tile-wide smallest |r| and largest key sum decide whether the tree sums
+    // are exact.
+    double tmax = t < kDim ? key_sum[t] : 0.0;
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+      min_abs = fminf(min_abs, __shfl_xor(min_abs, mask));
+      tmax = fmax(tmax, __shfl_xor(tmax, mask));
+    }
+    if (lane == 0) {
+      min_part[wave] = min_abs;
+      tmax_part[wave] = tmax;
+    }
+    __syncthreads();
+    min_abs = fminf(fminf(min_part[0], min_part[1]),
+                    fminf(min_part[2], min_part[3]));
+    tmax = fmax(fmax(tmax_part[0], tmax_part[1]),
+                fmax(tmax_part[2], tmax_part[3]));
+    bool exact = tmax == 0.0;
+    if (!exact && min_abs > 0.0f) {
+      const int e = granularity_exponent(min_abs) + 29;
+      const double bound =
+          __longlong_as_double(static_cast<long long>(e + 1023) << 52);
+      exact = tmax < bound;
+    }
+    if (!exact) {
+      if (t < kDim) key_sum[t] = serial_key_sum<kLayout>(tile, t);
+      __syncthreads();
+    }
+    if (t < kDim) {
+      const float mean = static_cast<float>(key_sum[t] / 128.0);
+      const float s = sqrtf(mean < kSmoothingFloor ? kSmoothingFloor : mean);
+      s_shared[t] = s;
+      s_inverse[t] = 1.0f / s;
+      smoothing[item * kDim + t] = s;
+    }
+    if constexpr (kMode == kModeSmoothingOnly) return;
+    // Markstein division is exact for every r / s when the smallest |r| is at
+    // least 2^-100 and s <= 2^20 (key sums <= 2^46): |r/s| <= 128 s stays far
+    // from overflow and >= 2^-120 stays normal.
+    fast_divide = min_abs >= 0x1p-100f && tmax <= 0x1p46;
+  } else {
+    if (t < kDim) {
+      const float s = given_smoothing[item * kDim + t];
+      s_shared[t] = s;
+      s_inverse[t] = 1.0f / s;
+    }
+  }
+  __syncthreads();
+
+  // ---- m = r / s -----------------------------------------------------------
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
+      const float s = s_shared[key];
+      x[j][i] = fast_divide ? div_by_reciprocal(x[j][i], s, s_inverse[key])
+                            : x[j][i] / s;
+    }
+  }
+
+  // ---- per-value scales: max |m| over keys --------------------------------
+  if constexpr (kLayout == kKeyValue) {
+    float mx[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float m = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kRowsPerThread; ++j) m = fmaxf(m, fabsf(x[j][i]));
+      mx[i] = fmaxf(m, __shfl_xor(m, 32));
+    }
+    if (lane < 32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) max_part[wave][4 * c4 + i] = mx[i];
+    }
+    __syncthreads();
+    if (t < kDim) {
+      scale_shared[t] = fmaxf(fmaxf(max_part[0][t], max_part[1][t]),
+                              fmaxf(max_part[2][t], max_part[3][t]));
+    }
+  } else {
+    float mx[kRowsPerThread];
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+      mx[j] = fmaxf(fmaxf(fabsf(x[j][0]), fabsf(x[j][1])),
+                    fmaxf(fabsf(x[j][2]), fabsf(x[j][3])));
+    }
+    reduce_rows_over_half_wave(mx, c4, MaxOp{});
+    if ((c4 & 1) == 0) scale_shared[8 * ((c4 >> 1) & 15) + group] = mx[0];
+  }
+  __syncthreads();
+  bool scale_ok = true;
+  if (t < kDim) {
+    const float scale = scale_shared[t];
+    scale_inverse[t] = scale == 0.0f ? 0.0f : 1.0f / scale;
+    scales[item * kDim + t] = scale;
+    scale_ok = scale == 0.0f || (scale >= 0x1p-90f && scale <= 0x1p90f);
+  }
+  // Markstein for m / scale: exact when 2^-90 <= scale <= 2^90 and |m| is
+  // large enough for the code to be non-zero; smaller |m| give |m/scale*127|
+  // < 0.5 on both paths.  scale == 0 gives y = 0 and code 0 like the reference.
+  const bool fast_scale = __syncthreads_and(scale_ok) != 0;
+
+  // ---- codes ---------------------------------------------------------------
+  int8_t* out = codes + item * kTile;
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int value = kLayout == kKeyValue ? 4 * c4 + i : 8 * j + group;
+      const float scale = scale_shared[value];
+      float q;
+      if (fast_scale) {
+        q = div_by_reciprocal(x[j][i], scale, scale_inverse[value]);
+      } else {
+        q = scale == 0.0f ? 0.0f : x[j][i] / scale;
+      }
+      const int code = round_half_away_small(q * kQuantizedMaximum);
+      packed |= (static_cast<uint32_t>(code) & 0xFFu) << (8 * i);
+    }
+    *reinterpret_cast<uint32_t*>(out + (8 * j + group) * kDim + 4 * c4) =
+        packed;
+  }
+}
+
+template <uint32_t kLayout, typename Out, bool kCompensated>
+__global__ __launch_bounds__(kThreads) void decode_kernel(
+    const int8_t* __restrict__ codes, const float* __restrict__ smoothing,
+    const float* __restrict__ scales,
+    const float* __restrict__ compensator_keys,
+    const float* __restrict__ compensator_values, Out* __restrict__ dense,
+    TileMap map) {
+  constexpr int kRank = 4;
+  __shared__ float s_shared[kDim];
+  __shared__ float scale_shared[kDim];
+  __shared__ float ck_shared[kCompensated ? kDim * kRank : 1];
+  __shared__ float cv_shared[kCompensated ? kDim * kRank : 1];
+
+  const uint64_t item = blockIdx.x;
+  uint64_t entry;
+  if (!pool_entry(map, item, &entry)) return;  // uniform over the workgroup
+
+  const int t = threadIdx.x;
+  const int group = t >> 5;
+  const int c4 = t & 31;
+
+  bool ok = true;
+  if (t < kDim) {
+    const float s = smoothing[item * kDim + t];
+    s_shared[t] = s;
+    // Markstein division by 127 is exact for s * code when s is in
+    // [2^-90, 2^100] (so the product is +0 or at least 2^-90 in magnitude).
+    ok = s >= 0x1p-90f && s <= 0x1p100f;
+  } else {
+    scale_shared[t - kDim] = scales[item * kDim + (t - kDim)];
+  }
+  if constexpr (kCompensated) {
+    for (int i = t; i < kDim * kRank; i += kThreads) {
+      ck_shared[i] = compensator_keys[item * kDim * kRank + i];
+      cv_shared[i] = compensator_values[item * kDim * kRank + i];
+    }
+  }
+  const bool fast_divide = __syncthreads_and(ok) != 0;
+
+  const int8_t* tile = codes + item * kTile;
+  Out* out = dense + entry * kTile;
+#pragma unroll 4
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const int row = 8 * j + group;
+    const uint32_t packed =
+        *reinterpret_cast<const uint32_t*>(tile + row * kDim + 4 * c4);
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = kLayout == kKeyValue ? row : 4 * c4 + i;
+      const int value = kLayout == kKeyValue ? 4 * c4 + i : row;
+      const float code = static_cast<float>(
+          static_cast<int8_t>(static_cast<uint8_t>(packed >> (8 * i))));
+      const float a = s_shared[key] * code;
+      const float d = fast_divide
+                          ? div_by_reciprocal(a, kQuantizedMaximum,
+                                              kInvQuantizedMaximum)
+                          : a / kQuantizedMaximum;
+      float value_out = d * scale_shared[value];
+      if constexpr (kCompensated) {
+#pragma unroll
+        for (int r = 0; r < kRank; ++r) {
+          value_out += ck_shared[key * kRank + r] * cv_shared[value * kRank + r];
+        }
+      }
+      v[i] = value_out;
+    }
+    store4(out + row * kDim + 4 * c4, v);
+  }
+}
+
+// --------------------------------------------------------------- dispatch
+
+template <int kMode>
+int32_t launch_encode(void* stream, const void* source, uint32_t dtype,
+                      int8_t* codes, float* smoothing, float* scales,
+                      const float* given_smoothing, uint64_t items,
+                      uint32_t layout, TileMap map) {
+  const dim3 grid(static_cast<uint32_t>(items));
+  const dim3 block(kThreads);
+  if (dtype == kDtypeF32) {
+    const float* src = static_cast<const float*>(source);
+    return layout == kKeyValue
+               ? launch(encode_kernel<kKeyValue, float, kMode>, grid, block,
+                        stream, src, codes, smoothing, scales, given_smoothing,
+                        map)
+               : launch(encode_kernel<kValueKey, float, kMode>, grid, block,
+                        stream, src, codes, smoothing, scales, given_smoothing,
+                        map);
+  }
+  const uint16_t* src = static_cast<const uint16_t*>(source);
+  return layout == kKeyValue
+             ? launch(encode_kernel<kKeyValue, uint16_t, kMode>, grid, block,
+                      stream, src, codes, smoothing, scales, given_smoothing,
+                      map)
+             : launch(encode_kernel<kValueKey, uint16_t, kMode>, grid, block,
+                      stream, src, codes, smoothing, scales, given_smoothing,
+                      map);
+}
+
+template <bool kCompensated>
+int32_t launch_decode(void* stream, const int8_t* codes, const float* smoothing,
+                      const float* scales, const float* compensator_keys,
+                      const float* compensator_values, void* dense,
+                      uint32_t dtype, uint64_t items, uint32_t layout,
+                      TileMap map) {
+  const dim3 grid(static_cast<uint32_t>(items));
+  const dim3 block(kThreads);
+  if (dtype == kDtypeF32) {
+    float* dst = static_cast<float*>(dense);
+    return layout == kKeyValue
+               ? launch(decode_kernel<kKeyValue, float, kCompensated>, grid,
+                        block, stream, codes, smoothing, scales,
+                        compensator_keys, compensator_values, dst, map)
+               : launch(decode_kernel<kValueKey, float, kCompensated>, grid,
+                        block, stream, codes, smoothing, scales,
+                        compensator_keys, compensator_values, dst, map);
+  }
+  uint16_t* dst = static_cast<uint16_t*>(dense);
+  return layout == kKeyValue
+             ? launch(decode_kernel<kKeyValue, uint16_t, kCompensated>, grid,
+                      block, stream, codes, smoothing, scales,
+                      compensator_keys, compensator_values, dst, map)
+             : launch(decode_kernel<kValueKey, uint16_t, kCompensated>, grid,
+                      block, stream, codes, smoothing, scales,
+                      compensator_keys, compensator_values, dst, map);
+}
+
+constexpr TileMap kIdentityMap{nullptr, 0, 0, 0};
+
+bool valid_layout(uint32_t layout) {
+  return layout == kKeyValue || layout == kValueKey;
+}
+
+// Reference admission for the provider launchers:
+// gdn_state_codec_quantize.cpp:207-211, gdn_state_codec_smoothing.cpp:144-147.
+bool provider_states_ok(uint32_t states) { return states >= 1 && states <= 64; }
+
+}  // namespace
+}  // namespace gdn
+
+using gdn::kStatusInvalidArgument;
+
+// ------------------------------------------------------ reference v1/v2 ABI
+
+extern "C" int32_t statecentric_gdn_state_codec_smoothing_launch_v1(
+    void* stream, const float* residual, float* smoothing) {
+  if (residual == nullptr || smoothing == nullptr) return kStatusInvalidArgument;
+  return gdn::launch_encode<gdn::kModeSmoothingOnly>(
+      stream, residual, gdn::kDtypeF32, nullptr, smoothing, nullptr, nullptr, 1,
+      gdn::kKeyValue, gdn::kIdentityMap);
+}
+
+extern "C" int32_t statecentric_gdn_state_codec_quantize_launch_v1(
+    void* stream, const float* residual, const float* smoothing,
+    int8_t* quantized, float* value_scales) {
+  if (residual == nullptr || smoothing == nullptr || quantized == nullptr ||
+      value_scales == nullptr) {
+    return kStatusInvalidArgument;
+  }
+  return gdn::launch_encode<gdn::kModeGivenSmoothing>(
+      stream, residual, gdn::kDtypeF32, quantized, nullptr, value_scales,
+      smoothing, 1, gdn::kKeyValue, gdn::kIdentityMap);
+}
+
+extern "C" int32_t statecentric_gdn_state_codec_dequantize_launch_v1(
+    void* stream, const int8_t* quantized, const float* smoothing,
+    const float* value_scales, const float* compensator_keys,
+    const float* compensator_values, float* dense) {
+  if (quantized == nullptr || smoothing == nullptr || value_scales == nullptr ||
+      compensator_keys == nullptr || compensator_values == nullptr ||
+      dense == nullptr) {
+    return kStatusInvalidArgument;
+  }
+  return gdn::launch_decode<true>(stream, quantized, smoothing, value_scales,
+                                  compensator_keys, compensator_values, dense,
+                                  gdn::kDtypeF32, 1, gdn::kKeyValue,
+                                  gdn::kIdentityMap);
+}
+
+extern "C" int32_t statecentric_gdn_state_codec_provider_smoothing_launch_v2(
+    void* stream, const float* provider_state, float* smoothing,
+    uint32_t states) {
+  if (provider_state == nullptr || smoothing == nullptr ||
+      !gdn::provider_states_ok(states)) {
+    return kStatusInvalidArgument;
+  }
+  return gdn::launch_encode<gdn::kModeSmoothingOnly>(
+      stream, provider_state, gdn::kDtypeF32, nullptr, smoothing, nullptr,
+      nullptr, states, gdn::kValueKey, gdn::kIdentityMap);
+}
+
+extern "C" int32_t statecentric_gdn_state_codec_provider_quantize_launch_v2(
+    void* stream, const float* provider_state, const float* smoothing,
+    int8_t* quantized, float* value_scales, uint32_t states) {
+  if (provider_state == nullptr || smoothing == nullptr ||
+      quantized == nullptr || value_scales == nullptr ||
+      !gdn::provider_states_ok(states)) {
+    return kStatusInvalidArgument;
+  }
+  return gdn::launch_encode<gdn::kModeGivenSmoothing>(
+      stream, provider_state, gdn::kDtypeF32, quantized, nullptr, value_scales,
+      smoothing, states, gdn::kValueKey, gdn::kIdentityMap);
+}
+
+// ------------------------------------------------------------ batched v4 ABI
+
+extern "C" int32_t statecentric_gdn_state_codec_encode_launch_v4(
+    void* stream, const float* state, int8_t* quantized, float* smoothing,
+    float* value_scales, uint64_t heads, uint32_t layout) {
+  if (state == nullptr || quantized == nullptr || smoothing == nullptr ||
+      value_scales == nullptr || heads == 0 || heads > gdn::kMaxGrid ||
+      !gdn::valid_layout(layout)) {
+    return kStatusInvalidArgument;
+  }
+  return gdn::launch_encode<gdn::kModeEncode>(
+      stream, state, gdn::kDtypeF32, quantized, smoothing, value_scales,
+      nullptr, heads, layout, gdn::kIdentityMap);
+}
+
+extern "C" int32_t statecentric_gdn_state_codec_decode_launch_v4(
+    void* stream, const int8_t* quantized, const float* smoothing,
+    const float* value_scales, const float* compensator_keys,
+    const float* compensator_values, float* state, uint64_t heads,
+    uint32_t layout) {
+  if (quantized == nullptr || smoothing == nullptr || value_scales == nullptr ||
+      state == nullptr || heads == 0 || heads > gdn::kMaxGrid ||
+      !gdn::valid_layout(layout) ||
+      (compensator_keys == nullptr) != (compensator_values == nullptr)) {
+    return kStatusInvalidArgument;
+  }
+  if (compensator_keys != nullptr) {
+    return gdn::launch_decode<true>(stream, quantized, smoothing, value_scales,
+                                    compensator_keys, compensator_values, state,
+                                    gdn::kDtypeF32, heads, layout,
+                                    gdn::kIdentityMap);
+  }
+  return gdn::launch_decode<false>(stream, quantized, smoothing, value_scales,
+                                   nullptr, nullptr, state, gdn::kDtypeF32,
+                                   heads, layout, gdn::kIdentityMap);
+}
+
+namespace {
+bool pool_args_ok(const int32_t* slot_ids, uint32_t batch, uint32_t layers,
+                  uint32_t slots, uint32_t heads, uint32_t layout,
+                  uint32_t dtype) {
+  if (slot_ids == nullptr || batch == 0 || layers == 0 || slots == 0 ||
+      heads == 0 || !gdn::valid_layout(layout) ||
+      (dtype != gdn::kDtypeF32 && dtype != gdn::kDtypeBF16)) {
+    return false;
+  }
+  const uint64_t items = static_cast<uint64_t>(layers) * batch * heads;
+  return items <= gdn::kMaxGrid;
+}
+}  // namespace
+
+extern "C" int32_t statecentric_gdn_state_codec_pool_encode_launch_v4(
+    void* stream, const void* pool, uint32_t pool_dtype,
+    const int32_t* slot_ids, uint32_t batch, uint32_t layers, uint32_t slots,
+    uint32_t heads, uint32_t layout, int8_t* quantized, float* smoothing,
+    float* value_scales) {
+  if (pool == nullptr || quantized == nullptr || smoothing == nullptr ||
+      value_scales == nullptr ||
+      !pool_args_ok(slot_ids, batch, layers, slots, heads, layout, pool_dtype)) {
+    return kStatusInvalidArgument;
+  }
+  const gdn::TileMap map{slot_ids, batch, heads, slots};
+  return gdn::launch_encode<gdn::kModeEncode>(
+      stream, pool, pool_dtype, quantized, smoothing, value_scales, nullptr,
+      static_cast<uint64_t>(layers) * batch * heads, layout, map);
+}
+
+extern "C" int32_t statecentric_gdn_state_codec_pool_decode_launch_v4(
+    void* stream, const int8_t* quantized, const float* smoothing,
+    const float* value_scales, const int32_t* slot_ids, uint32_t batch,
+    uint32_t layers, uint32_t slots, uint32_t heads, uint32_t layout,
+    void* pool, uint32_t pool_dtype) {
+  if (pool == nullptr || quantized == nullptr || smoothing == nullptr ||
+      value_scales == nullptr ||
+      !pool_args_ok(slot_ids, batch, layers, slots, heads, layout, pool_dtype)) {
+    return kStatusInvalidArgument;
+  }
+  const gdn::TileMap map{slot_ids, batch, heads, slots};
+  return gdn::launch_decode<false>(
+      stream, quantized, smoothing, value_scales, nullptr, nullptr, pool,
+      pool_dtype, static_cast<uint64_t>(layers) * batch * heads, layout, map);
+}

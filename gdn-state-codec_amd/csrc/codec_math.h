@@ -1,0 +1,79 @@
+// Scalar arithmetic shared by the codec kernels, written so the same code can be
+// compiled for the host (tests/test_codec_math.py builds it with g++ and checks
+// it exhaustively against IEEE division and std::lround).
+//
+// Bit-exactness contract: the codec reproduces the reference's portable C++
+// quant stage (native/src/gdn_state_codec_state_capsule.cpp:190-251), which
+// divides with IEEE fp32 division and rounds with std::lround.  The helpers
+// below are drop-in replacements that are exact on the domains stated at each
+// one; callers fall back to plain `/` outside those domains.
+#pragma once
+
+#include <math.h>
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define GDN_HD __host__ __device__ __forceinline__
+#else
+#define GDN_HD inline
+#endif
+
+namespace gdn {
+
+// Quotient a / b from y = RN(1/b) with one residual correction (Markstein 1990,
+// "Computation of elementary functions on the IBM RISC System/6000 processor"):
+//   q0 = RN(a*y);  r = a - b*q0 (exact, one fma);  q = RN(q0 + r*y).
+// It equals RN(a/b) when y = RN(1/b), 2^-100 <= |a| <= 2^120,
+// 2^-90 <= |b| <= 2^90 and 2^-120 <= |a/b| <= 2^120: then b*q0 has no bits
+// below 2^-149, so r is exactly representable, and no step overflows or
+// underflows, which is the theorem's premise.  a == +0 yields +0; a == -0
+// yields +0 where IEEE gives -0, so callers keep -0 out (or only use the
+// result through fabs or an integer rounding, where the sign cannot show).
+GDN_HD float div_by_reciprocal(float a, float b, float y) {
+  const float q0 = a * y;
+  const float r = fmaf(-q0, b, a);
+  return fmaf(r, y, q0);
+}
+
+// std::lround for |x| <= 127, returned as int: truncation of x + copysign(c, x)
+// with c = 0.5 - 2^-25 (the largest float below 0.5).  Using 0.5 itself would
+// round x = 0.5 - 2^-25 up to 1; with c every half-integer still rounds away
+// from zero because n + 0.5 + c lies within half an ulp of n + 1 for n >= 1,
+// and 0.5 + c = 1 - 2^-25 ties to the even 1.0.  Verified for every float in
+// [-127, 127] by tests/test_codec_math.py.
+GDN_HD int round_half_away_small(float x) {
+  const float c = copysignf(0.49999997f, x);
+  return static_cast<int>(x + c);
+}
+
+// Largest positive quantized magnitude (kQuantizedMaximum,
+// state_capsule.cpp:20) and its correctly rounded reciprocal.
+constexpr float kQuantizedMaximum = 127.0f;
+constexpr float kInvQuantizedMaximum = 1.0f / 127.0f;
+
+// Reference smoothing floor (GdnStateCodecParameters::smoothing_floor,
+// gdn_state_codec_state_capsule.h:17).
+constexpr float kSmoothingFloor = 1.0e-8f;
+
+// bf16 <-> fp32.  Widening is exact; narrowing rounds to nearest even exactly as
+// the reference's FloatToBFloat16 (windowed_gdn_step.cpp:26-32).
+GDN_HD float bf16_to_float(uint16_t bits) {
+  union {
+    uint32_t u;
+    float f;
+  } v;
+  v.u = static_cast<uint32_t>(bits) << 16;
+  return v.f;
+}
+
+GDN_HD uint16_t float_to_bf16(float value) {
+  union {
+    uint32_t u;
+    float f;
+  } v;
+  v.f = value;
+  const uint32_t lsb = (v.u >> 16) & 1u;
+  return static_cast<uint16_t>((v.u + 0x7FFFu + lsb) >> 16);
+}
+
+}  // namespace gdn

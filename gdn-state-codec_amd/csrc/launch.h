@@ -1,0 +1,57 @@
+// Kernel-launch plumbing shared by the C-ABI entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <tuple>
+
+namespace gdn {
+
+// Status codes of every extern "C" entry point.  0 and 1 are the reference's
+// (gdn_state_codec_quantize.cpp:207-211: 1 = null pointer or out-of-range
+// count); 5 reports a HIP launch failure, which the reference's AscendC
+// launches cannot observe.
+constexpr int32_t kStatusOk = 0;
+constexpr int32_t kStatusInvalidArgument = 1;
+constexpr int32_t kStatusLaunchFailed = 5;
+
+// Tile geometry: one Qwen3.5 GDN head is a 128 x 128 fp32 matrix.
+constexpr int kDim = 128;
+constexpr int kTile = kDim * kDim;
+
+// Tile layouts.  kKeyValue is the codec/capsule layout [key][value]
+// (gdn_state_codec_qwen38_gdn_adapter.h:10-11); kValueKey is the Qwen provider
+// layout [value][key] (runtime.py:378, 407-408).
+constexpr uint32_t kKeyValue = 0;
+constexpr uint32_t kValueKey = 1;
+
+// Pool element types.
+constexpr uint32_t kDtypeF32 = 0;
+constexpr uint32_t kDtypeBF16 = 1;
+
+// Largest grid the launchers issue along x (hardware limit 2^31 - 1).
+constexpr uint64_t kMaxGrid = 0x7FFFFFFFull;
+
+// Launches `kernel` on `stream` through hipLaunchKernel so the launch status
+// comes back to the caller instead of staying in the thread's last-error slot.
+// Arguments are converted to the kernel's parameter types first.
+template <typename... KernelArgs, typename... Args>
+int32_t launch(void (*kernel)(KernelArgs...), dim3 grid, dim3 block,
+               void* stream, Args... args) {
+  static_assert(sizeof...(KernelArgs) == sizeof...(Args), "argument count");
+  std::tuple<KernelArgs...> values(static_cast<KernelArgs>(args)...);
+  void* pointers[sizeof...(KernelArgs)];
+  std::apply(
+      [&pointers](auto&... value) {
+        int index = 0;
+        ((pointers[index++] = static_cast<void*>(&value)), ...);
+      },
+      values);
+  const hipError_t status =
+      hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block,
+                      pointers, 0, static_cast<hipStream_t>(stream));
+  return status == hipSuccess ? kStatusOk : kStatusLaunchFailed;
+}
+
+}  // namespace gdn

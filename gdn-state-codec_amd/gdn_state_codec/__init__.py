@@ -1,0 +1,32 @@
+"""MI355X (gfx950) GDN state codec: int8 codec of Qwen3.5 gated-delta-net
+recurrent-state head tiles and the encoded projection, behind the reference's
+``statecentric_gdn_state_codec_*`` C-ABI."""
+
+from ._native import NativeLibrary, library_dir, library_path, native
+from .codec import (
+    LAYOUT_KEY_VALUE,
+    LAYOUT_VALUE_KEY,
+    decode,
+    encode,
+    pool_decode,
+    pool_encode,
+    project_chunked,
+    project_decode,
+)
+from .runtime import GdnStateCodecRuntime
+
+__all__ = [
+    "LAYOUT_KEY_VALUE",
+    "LAYOUT_VALUE_KEY",
+    "GdnStateCodecRuntime",
+    "NativeLibrary",
+    "decode",
+    "encode",
+    "library_dir",
+    "library_path",
+    "native",
+    "pool_decode",
+    "pool_encode",
+    "project_chunked",
+    "project_decode",
+]

@@ -1,0 +1,87 @@
+"""ctypes bindings of the gfx950 C-ABI library (``include/*.h``).
+
+The library is loaded from ``$GDN_STATE_CODEC_LIBRARY_DIR`` when set (the
+reference's variable, ``manifests/vllm-hust-extension-v0.3.json:58-63``) and
+otherwise from the in-tree ``lib/`` directory built by ``build.py``.  A missing
+library raises: there is no CPU or torch fallback on the product path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent.parent
+DEFAULT_LIBRARY_DIR = PACKAGE_DIR / "lib"
+LIBRARY_NAME = "libstatecentric_gdn_state_codec.so"
+
+_P = ctypes.c_void_p
+_U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
+_F = ctypes.c_float
+_I32 = ctypes.c_int32
+
+# name -> argtypes (all return int32 status)
+SIGNATURES: dict[str, list] = {
+    # codec, reference entry points
+    "statecentric_gdn_state_codec_smoothing_launch_v1": [_P, _P, _P],
+    "statecentric_gdn_state_codec_provider_smoothing_launch_v2": [_P, _P, _P, _U32],
+    "statecentric_gdn_state_codec_quantize_launch_v1": [_P, _P, _P, _P, _P],
+    "statecentric_gdn_state_codec_provider_quantize_launch_v2": [_P, _P, _P, _P, _P, _U32],
+    "statecentric_gdn_state_codec_provider_initialize_launch_v3": [_P, _P, _P, _P, _P, _U32],
+    "statecentric_gdn_state_codec_dequantize_launch_v1": [_P, _P, _P, _P, _P, _P, _P],
+    # codec, batched
+    "statecentric_gdn_state_codec_encode_launch_v4": [_P, _P, _P, _P, _P, _U64, _U32],
+    "statecentric_gdn_state_codec_decode_launch_v4": [_P, _P, _P, _P, _P, _P, _P, _U64, _U32],
+    "statecentric_gdn_state_codec_pool_encode_launch_v4": [
+        _P, _P, _U32, _P, _U32, _U32, _U32, _U32, _U32, _P, _P, _P],
+    "statecentric_gdn_state_codec_pool_decode_launch_v4": [
+        _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _P, _U32],
+    # encoded projection
+    "statecentric_gdn_state_codec_encoded_projection_decode_launch_v4": [
+        _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _F, _U32],
+    "statecentric_gdn_state_codec_encoded_projection_chunked_launch_v4": [
+        _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _F, _U32],
+}
+
+
+def library_dir() -> Path:
+    override = os.environ.get("GDN_STATE_CODEC_LIBRARY_DIR")
+    return Path(override) if override else DEFAULT_LIBRARY_DIR
+
+
+def library_path() -> Path:
+    return library_dir() / LIBRARY_NAME
+
+
+class NativeLibrary:
+    """The loaded library with typed entry points as attributes."""
+
+    def __init__(self, path: Path | None = None) -> None:
+        path = path or library_path()
+        if not path.is_file():
+            raise RuntimeError(
+                f"GDN State Codec native library is missing: {path} "
+                "(run gdn-state-codec_amd/build.py)"
+            )
+        self.path = path
+        self._lib = ctypes.CDLL(str(path))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(self._lib, name)
+            fn.argtypes = argtypes
+            fn.restype = _I32
+            setattr(self, name.removeprefix("statecentric_gdn_state_codec_"), fn)
+
+    def symbol(self, name: str):
+        return getattr(self._lib, name)
+
+
+_library: NativeLibrary | None = None
+
+
+def native() -> NativeLibrary:
+    global _library
+    if _library is None:
+        _library = NativeLibrary()
+    return _library

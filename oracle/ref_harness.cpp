@@ -1,0 +1,189 @@
+// Test infrastructure only: a C-ABI harness around the reference's portable C++
+// CPU path, compiled from the reference sources where they lie (never copied).
+// It is built by oracle/Makefile into oracle/_ref/ and used only by
+// tests/golden/make_golden.py, the oracle-vs-reference tests and bench.py's
+// cpu_baseline leg.  The product path never loads it.
+//
+// The quant-only stage of the codec is the anonymous-namespace function
+// QuantizeBoundary (native/src/gdn_state_codec_state_capsule.cpp:129-227); it is
+// reachable only from inside that translation unit, so this harness includes
+// the .cpp (by include path, -I $(REF)/native/src) instead of linking it.
+#include "gdn_state_codec_state_capsule.cpp"
+
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <vector>
+
+#include "statecentric/gdn_state_codec_qwen38_gdn_adapter.h"
+
+namespace {
+
+statecentric::GdnStateCodecIdentity MakeIdentity(std::uint32_t keys,
+                                                 std::uint32_t values) {
+  return {std::string(64, 'a'), 1, 1, keys, values};
+}
+
+statecentric::GdnStateCodecParameters MakeParameters(std::uint32_t rank) {
+  statecentric::GdnStateCodecParameters parameters;
+  parameters.compensator_rank = rank;
+  return parameters;
+}
+
+}  // namespace
+
+extern "C" {
+
+// QuantizeBoundary with compensator_rank = rank (0 = the quant-only
+// initializer: the residual is the dense state itself).  Layout [K][V].
+int gdnref_quantize_boundary(const float* dense, std::uint32_t keys,
+                             std::uint32_t values, std::uint32_t rank,
+                             std::int8_t* residual, float* smoothing,
+                             float* value_scales, float* compensator_keys,
+                             float* compensator_values) {
+  try {
+    const auto identity = MakeIdentity(keys, values);
+    const auto parameters = MakeParameters(rank);
+    const auto boundary = statecentric::QuantizeBoundary(
+        std::span<const float>(dense, std::size_t{keys} * values), identity,
+        parameters);
+    std::memcpy(residual, boundary->residual.data(), boundary->residual.size());
+    std::memcpy(smoothing, boundary->smoothing.data(), keys * sizeof(float));
+    std::memcpy(value_scales, boundary->value_scales.data(),
+                values * sizeof(float));
+    if (rank > 0) {
+      std::memcpy(compensator_keys, boundary->compensator_keys.data(),
+                  std::size_t{keys} * rank * sizeof(float));
+      std::memcpy(compensator_values, boundary->compensator_values.data(),
+                  std::size_t{values} * rank * sizeof(float));
+    }
+    return 0;
+  } catch (const std::exception&) {
+    return 1;
+  }
+}
+
+// DequantizeBoundary (state_capsule.cpp:229-251).  Compensators may be null
+// when rank == 0.
+int gdnref_dequantize_boundary(const std::int8_t* residual,
+                               const float* smoothing,
+                               const float* value_scales,
+                               const float* compensator_keys,
+                               const float* compensator_values,
+                               std::uint32_t keys, std::uint32_t values,
+                               std::uint32_t rank, float* dense) {
+  try {
+    const auto identity = MakeIdentity(keys, values);
+    const auto parameters = MakeParameters(rank);
+    statecentric::GdnStateCodecCapsule::Boundary boundary;
+    boundary.residual.assign(residual, residual + std::size_t{keys} * values);
+    boundary.smoothing.assign(smoothing, smoothing + keys);
+    boundary.value_scales.assign(value_scales, value_scales + values);
+    if (rank > 0) {
+      boundary.compensator_keys.assign(
+          compensator_keys, compensator_keys + std::size_t{keys} * rank);
+      boundary.compensator_values.assign(
+          compensator_values, compensator_values + std::size_t{values} * rank);
+    }
+    const auto out = statecentric::DequantizeBoundary(boundary, identity,
+                                                      parameters);
+    std::memcpy(dense, out.data(), out.size() * sizeof(float));
+    return 0;
+  } catch (const std::exception&) {
+    return 1;
+  }
+}
+
+// ReadWindowState with an empty record window (state_capsule.cpp:253-306):
+// the boundary readout S^T x of the encoded state.
+int gdnref_read_boundary(const std::int8_t* residual, const float* smoothing,
+                         const float* value_scales,
+                         const float* compensator_keys,
+                         const float* compensator_values, std::uint32_t keys,
+                         std::uint32_t values, std::uint32_t rank,
+                         const float* read, float* output) {
+  try {
+    const auto identity = MakeIdentity(keys, values);
+    const auto parameters = MakeParameters(rank);
+    statecentric::GdnStateCodecCapsule::Boundary boundary;
+    boundary.residual.assign(residual, residual + std::size_t{keys} * values);
+    boundary.smoothing.assign(smoothing, smoothing + keys);
+    boundary.value_scales.assign(value_scales, value_scales + values);
+    if (rank > 0) {
+      boundary.compensator_keys.assign(
+          compensator_keys, compensator_keys + std::size_t{keys} * rank);
+      boundary.compensator_values.assign(
+          compensator_values, compensator_values + std::size_t{values} * rank);
+    }
+    const std::vector<statecentric::GdnStateCodecCapsule::UpdateRecord> none;
+    const auto out = statecentric::ReadWindowState(
+        boundary, none, std::span<const float>(read, keys), identity,
+        parameters);
+    std::memcpy(output, out.data(), out.size() * sizeof(float));
+    return 0;
+  } catch (const std::exception&) {
+    return 1;
+  }
+}
+
+// Qwen provider [value][key] -> codec [key][value]
+// (gdn_state_codec_qwen38_gdn_adapter.cpp:21-38) and back (:40-57).
+int gdnref_provider_to_codec(const float* provider, std::uint32_t keys,
+                             std::uint32_t values, float* codec) {
+  try {
+    const auto out = statecentric::Qwen38ProviderStateToGdnStateCodec(
+        std::span<const float>(provider, std::size_t{keys} * values), keys,
+        values);
+    std::memcpy(codec, out.data(), out.size() * sizeof(float));
+    return 0;
+  } catch (const std::exception&) {
+    return 1;
+  }
+}
+
+int gdnref_codec_to_provider(const float* codec, std::uint32_t keys,
+                             std::uint32_t values, float* provider) {
+  try {
+    const auto out = statecentric::GdnStateCodecStateToQwen38Provider(
+        std::span<const float>(codec, std::size_t{keys} * values), keys,
+        values);
+    std::memcpy(provider, out.data(), out.size() * sizeof(float));
+    return 0;
+  } catch (const std::exception&) {
+    return 1;
+  }
+}
+
+// Batched quant-only encode over `heads` contiguous [K][V] tiles, used as the
+// reference CPU baseline (single thread, the reference's own code).
+int gdnref_quantize_heads(const float* dense, std::uint64_t heads,
+                          std::uint32_t keys, std::uint32_t values,
+                          std::int8_t* residual, float* smoothing,
+                          float* value_scales) {
+  const std::size_t tile = std::size_t{keys} * values;
+  for (std::uint64_t head = 0; head < heads; ++head) {
+    const int status = gdnref_quantize_boundary(
+        dense + head * tile, keys, values, 0, residual + head * tile,
+        smoothing + head * keys, value_scales + head * values, nullptr,
+        nullptr);
+    if (status != 0) return status;
+  }
+  return 0;
+}
+
+int gdnref_dequantize_heads(const std::int8_t* residual,
+                            const float* smoothing, const float* value_scales,
+                            std::uint64_t heads, std::uint32_t keys,
+                            std::uint32_t values, float* dense) {
+  const std::size_t tile = std::size_t{keys} * values;
+  for (std::uint64_t head = 0; head < heads; ++head) {
+    const int status = gdnref_dequantize_boundary(
+        residual + head * tile, smoothing + head * keys,
+        value_scales + head * values, nullptr, nullptr, keys, values, 0,
+        dense + head * tile);
+    if (status != 0) return status;
+  }
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,125 @@
+// Host build of gdn-state-codec_amd/csrc/codec_math.h, checked against IEEE
+// division and std::lround (built and run by tests/test_codec_math.py).
+//
+//   codec_math_check div127          every float a with 2^-100 <= |a| <= 2^120
+//                                    and a = +0: div_by_reciprocal(a, 127, RN(1/127))
+//                                    == a / 127
+//   codec_math_check divrandom N     N random divisors b in [2^-90, 2^90] x every
+//                                    significand of a, exponents chosen so that
+//                                    2^-120 <= |a/b| <= 2^120
+//   codec_math_check round           every float |x| <= 127: round_half_away_small(x)
+//                                    == clamp(lroundf(x), -127, 127)
+// Prints "<checked> <failures>" and exits non-zero on any failure.
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <atomic>
+#include <thread>
+#include <vector>
+
+#include "codec_math.h"
+
+namespace {
+
+float from_bits(uint32_t u) {
+  float f;
+  memcpy(&f, &u, sizeof f);
+  return f;
+}
+uint32_t to_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, sizeof u);
+  return u;
+}
+
+std::atomic<uint64_t> checked{0}, failures{0};
+
+template <typename Fn>
+void parallel(uint64_t begin, uint64_t end, Fn fn) {
+  const unsigned threads = std::max(1u, std::thread::hardware_concurrency());
+  std::vector<std::thread> pool;
+  for (unsigned t = 0; t < threads; ++t) {
+    pool.emplace_back([=] {
+      uint64_t local_checked = 0, local_failures = 0;
+      for (uint64_t i = begin + t; i < end; i += threads) fn(i, local_checked, local_failures);
+      checked += local_checked;
+      failures += local_failures;
+    });
+  }
+  for (auto& th : pool) th.join();
+}
+
+void check_div127() {
+  const float b = 127.0f;
+  const float y = 1.0f / b;
+  // biased exponents 27 (2^-100) .. 247 (2^120), both signs, every significand.
+  const uint64_t lo = static_cast<uint64_t>(27) << 23;
+  const uint64_t hi = static_cast<uint64_t>(248) << 23;
+  parallel(lo, hi, [&](uint64_t u, uint64_t& n, uint64_t& bad) {
+    for (uint32_t sign = 0; sign < 2; ++sign) {
+      const float a = from_bits(static_cast<uint32_t>(u) | (sign << 31));
+      ++n;
+      if (to_bits(gdn::div_by_reciprocal(a, b, y)) != to_bits(a / b)) ++bad;
+    }
+  });
+  checked += 1;
+  if (to_bits(gdn::div_by_reciprocal(0.0f, b, y)) != to_bits(0.0f / b)) ++failures;
+}
+
+void check_div_random(int divisors) {
+  srand(12345);
+  for (int d = 0; d < divisors; ++d) {
+    const uint32_t exponent = 127 - 90 + static_cast<uint32_t>(rand() % 181);
+    const uint32_t mantissa = ((static_cast<uint32_t>(rand()) << 12) ^ rand()) & 0x7FFFFFu;
+    const float b = from_bits((exponent << 23) | mantissa);
+    const float y = 1.0f / b;
+    // a exponent: pick one keeping |a| in [2^-100, 2^120] and |a/b| in range.
+    const int eb = static_cast<int>(exponent) - 127;
+    int ea = eb + (rand() % 61) - 30;
+    if (ea < -100) ea = -100;
+    if (ea > 119) ea = 119;
+    const uint32_t abits = static_cast<uint32_t>(ea + 127) << 23;
+    parallel(0, 1u << 23, [&](uint64_t m, uint64_t& n, uint64_t& bad) {
+      for (uint32_t step = 0; step < 2; ++step) {
+        const float a = from_bits(abits + (step << 23) + static_cast<uint32_t>(m));
+        ++n;
+        if (to_bits(gdn::div_by_reciprocal(a, b, y)) != to_bits(a / b)) ++bad;
+      }
+    });
+  }
+}
+
+void check_round() {
+  const uint64_t end = static_cast<uint64_t>(to_bits(127.0f)) + 1;
+  parallel(0, end, [&](uint64_t u, uint64_t& n, uint64_t& bad) {
+    for (uint32_t sign = 0; sign < 2; ++sign) {
+      const float x = from_bits(static_cast<uint32_t>(u) | (sign << 31));
+      long expect = lroundf(x);
+      if (expect < -127) expect = -127;
+      if (expect > 127) expect = 127;
+      ++n;
+      if (gdn::round_half_away_small(x) != expect) ++bad;
+    }
+  });
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc < 2) return 2;
+  if (strcmp(argv[1], "div127") == 0) {
+    check_div127();
+  } else if (strcmp(argv[1], "divrandom") == 0) {
+    check_div_random(argc > 2 ? atoi(argv[2]) : 64);
+  } else if (strcmp(argv[1], "round") == 0) {
+    check_round();
+  } else {
+    return 2;
+  }
+  printf("%llu %llu\n", static_cast<unsigned long long>(checked.load()),
+         static_cast<unsigned long long>(failures.load()));
+  return failures.load() == 0 ? 0 : 1;
+}

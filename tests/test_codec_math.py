@@ -1,0 +1,55 @@
+"""The device arithmetic of the codec (csrc/codec_math.h), compiled for the host
+and compared exhaustively with IEEE division and std::lround.
+
+The kernels replace `a / b` by a reciprocal multiply with one fma correction
+and `lround` by a truncating add; these tests are what licenses that."""
+
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+SOURCE = ROOT / "tests" / "codec_math_check.cpp"
+CSRC = ROOT / "gdn-state-codec_amd" / "csrc"
+
+
+def _has_fma() -> bool:
+    try:
+        return " fma " in Path("/proc/cpuinfo").read_text().replace("\n", " ")
+    except OSError:
+        return False
+
+
+@pytest.fixture(scope="module")
+def checker(tmp_path_factory):
+    if not _has_fma():
+        pytest.skip("host CPU has no FMA; the software fmaf is too slow for these sweeps")
+    binary = tmp_path_factory.mktemp("codec_math") / "codec_math_check"
+    subprocess.run(
+        ["g++", "-std=c++17", "-O2", "-mfma", "-ffp-contract=off", "-fno-fast-math",
+         "-pthread", f"-I{CSRC}", str(SOURCE), "-o", str(binary)],
+        check=True,
+    )
+    return binary
+
+
+def _run(binary, *args):
+    proc = subprocess.run([str(binary), *args], capture_output=True, text=True, timeout=600)
+    checked, failures = map(int, proc.stdout.split())
+    return proc.returncode, checked, failures
+
+
+def test_division_by_127_is_ieee_on_its_whole_domain(checker):
+    rc, checked, failures = _run(checker, "div127")
+    assert checked > 3_000_000_000 and failures == 0 and rc == 0
+
+
+def test_division_by_random_divisors_is_ieee(checker):
+    rc, checked, failures = _run(checker, "divrandom", "48")
+    assert checked == 48 * 2 * (1 << 23) and failures == 0 and rc == 0
+
+
+def test_rounding_matches_lround_for_every_float_up_to_127(checker):
+    rc, checked, failures = _run(checker, "round")
+    assert checked > 2_000_000_000 and failures == 0 and rc == 0

@@ -1,0 +1,127 @@
+"""GPU parity of the encoded projection (decode GEMV and chunked MFMA) against
+the oracle readout and the reference's golden readouts.
+
+Tolerance (fp32): |out - exact| <= 2^-15 * sum_k |code * s * x| * scale / 127,
+where exact is the fp64 evaluation of the same closed form from the same
+inputs; the fp32 oracle itself stays within 2^-17 of that magnitude."""
+
+import numpy as np
+import pytest
+import torch
+
+import datagen
+import oracle
+from gdn_state_codec import codec
+
+pytestmark = pytest.mark.gpu
+KV, VK = codec.LAYOUT_KEY_VALUE, codec.LAYOUT_VALUE_KEY
+TOL = 2.0 ** -15
+
+
+def to_gpu(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def to_np(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def _encoded(tiles_shape, seed, layout):
+    x = datagen.c1_heads(int(np.prod(tiles_shape)), seed)
+    if layout == VK:
+        x = np.ascontiguousarray(x.transpose(0, 2, 1))
+    codes, s, sc = oracle.encode_heads(x, layout, threads=8)
+    shape = tuple(tiles_shape)
+    return codes.reshape(shape + (128, 128)), s.reshape(shape + (128,)), sc.reshape(shape + (128,))
+
+
+def _queries(shape, seed):
+    g = datagen.rng(seed)
+    q = g.standard_normal(shape).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)  # L2-normalised per head
+    return oracle.f32_to_bf16(q)
+
+
+def _within(got, exact, bound):
+    err = np.abs(got.astype(np.float64) - exact)
+    return err <= TOL * bound + 1e-30
+
+
+@pytest.mark.parametrize("layout", [VK, KV])
+@pytest.mark.parametrize("batch,heads,qheads,qscale", [
+    (4, 32, 16, 1.0), (3, 32, 16, 128 ** -0.5), (5, 8, 8, 1.0), (2, 6, 2, 0.5)])
+def test_decode_projection_matches_oracle(device, layout, batch, heads, qheads, qscale):
+    print(f"decode projection layout={layout} B={batch} H={heads} Hq={qheads}", flush=True)
+    codes, s, sc = _encoded((batch, heads), 10 + batch, layout)
+    q = _queries((batch, qheads, 128), 20 + batch)
+    out32, out64, bound = oracle.project_decode(codes, s, sc, q, qscale, layout)
+    got = to_np(codec.project_decode(to_gpu(codes, device), to_gpu(s, device),
+                                     to_gpu(sc, device), to_gpu(q, device).view(torch.bfloat16),
+                                     qscale, layout))
+    assert _within(got, out64, bound).all()
+    assert _within(out32, out64, bound).all()
+
+
+def test_decode_projection_matches_reference_readouts(device, golden):
+    for name in golden["names"]:
+        codes = golden[f"{name}/codes"][None, None]
+        s = golden[f"{name}/smoothing"][None, None]
+        sc = golden[f"{name}/scales"][None, None]
+        q = golden[f"{name}/query_bf16"][None, None]
+        _, out64, bound = oracle.project_decode(codes, s, sc, q, 1.0, KV)
+        ref = golden[f"{name}/readout"]
+        got = to_np(codec.project_decode(to_gpu(codes, device), to_gpu(s, device),
+                                         to_gpu(sc, device), to_gpu(q, device).view(torch.bfloat16),
+                                         1.0, KV))[0, 0]
+        assert _within(got, out64[0, 0], bound[0, 0]).all(), name
+        assert _within(ref, out64[0, 0], bound[0, 0]).all(), name
+
+
+def test_decode_projection_full_config3(device):
+    """B=256, 16 query heads GQA-mapped to 32 value heads."""
+    codes, s, sc = _encoded((256, 32), 30, VK)
+    q = _queries((256, 16, 128), 31)
+    _, out64, bound = oracle.project_decode(codes, s, sc, q, 1.0, VK)
+    got = to_np(codec.project_decode(to_gpu(codes, device), to_gpu(s, device), to_gpu(sc, device),
+                                     to_gpu(q, device).view(torch.bfloat16), 1.0, VK))
+    assert _within(got, out64, bound).all()
+
+
+@pytest.mark.parametrize("layout", [VK, KV])
+@pytest.mark.parametrize("seqs,tokens,heads,qheads", [
+    (2, 64, 32, 32), (3, 37, 8, 4), (2, 1, 4, 4), (1, 96, 4, 2)])
+def test_chunked_projection_matches_oracle(device, layout, seqs, tokens, heads, qheads):
+    print(f"chunked projection layout={layout} N={seqs} T={tokens} H={heads} Hq={qheads}",
+          flush=True)
+    codes, s, sc = _encoded((seqs, heads), 40 + tokens, layout)
+    q = _queries((seqs, tokens, qheads, 128), 50 + tokens)
+    out32, out64, bound = oracle.project_chunked(codes, s, sc, q, 1.0, layout, threads=8)
+    got = to_np(codec.project_chunked(to_gpu(codes, device), to_gpu(s, device),
+                                      to_gpu(sc, device), to_gpu(q, device).view(torch.bfloat16),
+                                      1.0, layout))
+    assert _within(got, out64, bound).all()
+
+
+def test_chunked_projection_full_config4(device):
+    """64 sequences x T=64 x 32 heads."""
+    codes, s, sc = _encoded((64, 32), 60, VK)
+    q = _queries((64, 64, 32, 128), 61)
+    _, out64, bound = oracle.project_chunked(codes, s, sc, q, 1.0, VK, threads=8)
+    got = to_np(codec.project_chunked(to_gpu(codes, device), to_gpu(s, device),
+                                      to_gpu(sc, device), to_gpu(q, device).view(torch.bfloat16),
+                                      1.0, VK))
+    assert _within(got, out64, bound).all()
+
+
+def test_chunked_equals_decode_token_by_token(device):
+    codes, s, sc = _encoded((2, 8), 70, VK)
+    q = _queries((2, 5, 4, 128), 71)
+    g = [to_gpu(a, device) for a in (codes, s, sc)]
+    chunked = to_np(codec.project_chunked(*g, to_gpu(q, device).view(torch.bfloat16), 1.0, VK))
+    _, out64, bound = oracle.project_chunked(codes, s, sc, q, 1.0, VK)
+    for t in range(5):
+        dec = to_np(codec.project_decode(*g, to_gpu(q[:, t], device).view(torch.bfloat16),
+                                         1.0, VK))
+        assert _within(dec, out64[:, t], bound[:, t]).all()
+        assert _within(chunked[:, t], out64[:, t], bound[:, t]).all()
