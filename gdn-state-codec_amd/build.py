@@ -25,6 +25,8 @@ CSRC = PACKAGE_DIR / "csrc"
 LIB_DIR = PACKAGE_DIR / "lib"
 OBJ_DIR = LIB_DIR / "obj"
 LIBRARY_NAME = "libstatecentric_gdn_state_codec.so"
+# Bandwidth probes for bench.py only (csrc/bench/); not part of the C-ABI.
+PROBE_LIBRARY_NAME = "libgdn_state_codec_hbm_probe.so"
 
 # Reference library names (runtime.py:55-62, 72, 101, 131, 154, 182, 202, 224)
 # whose hot-path symbols this library exports.
@@ -58,7 +60,7 @@ def _sources() -> list[Path]:
 
 
 def _compile(source: Path) -> Path:
-    obj = OBJ_DIR / (source.stem + source.suffix.replace(".", "_") + ".o")
+    obj = OBJ_DIR / (source.parent.name + "_" + source.stem + source.suffix.replace(".", "_") + ".o")
     cmd = [HIPCC, *COMMON_FLAGS, "-c", str(source), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
@@ -70,21 +72,30 @@ def _compile(source: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile all sources and link the shared library; returns its path."""
-    OBJ_DIR.mkdir(parents=True, exist_ok=True)
-    sources = _sources()
-    jobs = min(len(sources), int(os.environ.get("MAX_JOBS", "8")), 16)
-    with ThreadPoolExecutor(max_workers=max(jobs, 1)) as pool:
-        objects = list(pool.map(_compile, sources))
-    target = LIB_DIR / LIBRARY_NAME
-    tmp = LIB_DIR / (LIBRARY_NAME + ".tmp")
+def _link(objects: list[Path], name: str) -> Path:
+    target = LIB_DIR / name
+    tmp = LIB_DIR / (name + ".tmp")
     link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC",
             *map(str, objects), "-o", str(tmp)]
     proc = subprocess.run(link, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, target)
+    return target
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile all sources and link the shared libraries; returns the codec's."""
+    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+    sources = _sources()
+    probes = sorted((CSRC / "bench").glob("*.hip"))
+    jobs = min(len(sources) + len(probes), int(os.environ.get("MAX_JOBS", "8")), 16)
+    with ThreadPoolExecutor(max_workers=max(jobs, 1)) as pool:
+        objects = list(pool.map(_compile, sources))
+        probe_objects = list(pool.map(_compile, probes))
+    target = _link(objects, LIBRARY_NAME)
+    if probe_objects:
+        _link(probe_objects, PROBE_LIBRARY_NAME)
     for name in REFERENCE_LIBRARY_NAMES:
         alias = LIB_DIR / name
         if alias.is_symlink() or alias.exists():

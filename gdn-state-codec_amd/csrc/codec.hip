@@ -28,6 +28,7 @@
 
 #include "codec_math.h"
 #include "launch.h"
+#include "stream_memory.h"
 
 namespace gdn {
 namespace {
@@ -73,7 +74,7 @@ __device__ __forceinline__ void load4(const T* p, float (&v)[4]);
 
 template <>
 __device__ __forceinline__ void load4<float>(const float* p, float (&v)[4]) {
-  const float4 q = *reinterpret_cast<const float4*>(p);
+  const float4 q = stream_load(reinterpret_cast<const float4*>(p));
   v[0] = q.x;
   v[1] = q.y;
   v[2] = q.z;
@@ -83,7 +84,7 @@ __device__ __forceinline__ void load4<float>(const float* p, float (&v)[4]) {
 template <>
 __device__ __forceinline__ void load4<uint16_t>(const uint16_t* p,
                                                 float (&v)[4]) {
-  const uint2 q = *reinterpret_cast<const uint2*>(p);
+  const uint2 q = stream_load(reinterpret_cast<const uint2*>(p));
   v[0] = bf16_to_float(static_cast<uint16_t>(q.x & 0xFFFFu));
   v[1] = bf16_to_float(static_cast<uint16_t>(q.x >> 16));
   v[2] = bf16_to_float(static_cast<uint16_t>(q.y & 0xFFFFu));
@@ -96,7 +97,7 @@ __device__ __forceinline__ float load1(const uint16_t* p) {
 }
 
 __device__ __forceinline__ void store4(float* p, const float (&v)[4]) {
-  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  stream_store(reinterpret_cast<float4*>(p), make_float4(v[0], v[1], v[2], v[3]));
 }
 
 __device__ __forceinline__ void store4(uint16_t* p, const float (&v)[4]) {
@@ -105,7 +106,7 @@ __device__ __forceinline__ void store4(uint16_t* p, const float (&v)[4]) {
         (static_cast<uint32_t>(float_to_bf16(v[1])) << 16);
   q.y = static_cast<uint32_t>(float_to_bf16(v[2])) |
         (static_cast<uint32_t>(float_to_bf16(v[3])) << 16);
-  *reinterpret_cast<uint2*>(p) = q;
+  stream_store(reinterpret_cast<uint2*>(p), q);
 }
 
 // One reduce-scatter step over lane pairs (lane, lane ^ mask) for an array of
@@ -168,6 +169,34 @@ __device__ double serial_key_sum(const In* tile, int key) {
     }
   }
   return sum;
+}
+
+// code = lround(m / scale * 127), packed four per 32-bit store (one row's
+// four consecutive columns).  kFast selects the reciprocal division.
+template <uint32_t kLayout, bool kFast>
+__device__ __forceinline__ void write_codes(const float (&x)[kRowsPerThread][4],
+                                            const float* scale_shared,
+                                            const float* scale_inverse,
+                                            int group, int c4, int8_t* out) {
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int value = kLayout == kKeyValue ? 4 * c4 + i : 8 * j + group;
+      const float scale = scale_shared[value];
+      float q;
+      if constexpr (kFast) {
+        q = div_by_reciprocal(x[j][i], scale, scale_inverse[value]);
+      } else {
+        q = scale == 0.0f ? 0.0f : x[j][i] / scale;
+      }
+      const int code = round_half_away_small(q * kQuantizedMaximum);
+      packed |= (static_cast<uint32_t>(code) & 0xFFu) << (8 * i);
+    }
+    stream_store(reinterpret_cast<uint32_t*>(out + (8 * j + group) * kDim + 4 * c4),
+                 packed);
+  }
 }
 
 template <uint32_t kLayout, typename In, int kMode>
@@ -294,14 +323,24 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   __syncthreads();
 
   // ---- m = r / s -----------------------------------------------------------
+  // The branch is uniform over the workgroup; each side is straight-line code.
+  if (fast_divide) {
 #pragma unroll
-  for (int j = 0; j < kRowsPerThread; ++j) {
+    for (int j = 0; j < kRowsPerThread; ++j) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
-      const float s = s_shared[key];
-      x[j][i] = fast_divide ? div_by_reciprocal(x[j][i], s, s_inverse[key])
-                            : x[j][i] / s;
+      for (int i = 0; i < 4; ++i) {
+        const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
+        x[j][i] = div_by_reciprocal(x[j][i], s_shared[key], s_inverse[key]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
+        x[j][i] = x[j][i] / s_shared[key];
+      }
     }
   }
 
@@ -349,24 +388,52 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
 
   // ---- codes ---------------------------------------------------------------
   int8_t* out = codes + item * kTile;
-#pragma unroll
+  if (fast_scale) {
+    write_codes<kLayout, true>(x, scale_shared, scale_inverse, group, c4, out);
+  } else {
+    write_codes<kLayout, false>(x, scale_shared, scale_inverse, group, c4, out);
+  }
+}
+
+// dense = ((s[k] * code) / 127) * scale[v] (+ sum_r ck[k][r] * cv[v][r]) for
+// the thread's 16 rows x 4 columns.  kFast selects the reciprocal division.
+template <uint32_t kLayout, bool kFast, bool kCompensated, typename Out>
+__device__ __forceinline__ void decode_rows(const int8_t* tile,
+                                            const float* s_shared,
+                                            const float* scale_shared,
+                                            const float* ck_shared,
+                                            const float* cv_shared, int group,
+                                            int c4, Out* out) {
+  constexpr int kRank = 4;
+#pragma unroll 4
   for (int j = 0; j < kRowsPerThread; ++j) {
-    uint32_t packed = 0;
+    const int row = 8 * j + group;
+    const uint32_t packed =
+        stream_load(reinterpret_cast<const uint32_t*>(tile + row * kDim + 4 * c4));
+    float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int value = kLayout == kKeyValue ? 4 * c4 + i : 8 * j + group;
-      const float scale = scale_shared[value];
-      float q;
-      if (fast_scale) {
-        q = div_by_reciprocal(x[j][i], scale, scale_inverse[value]);
+      const int key = kLayout == kKeyValue ? row : 4 * c4 + i;
+      const int value = kLayout == kKeyValue ? 4 * c4 + i : row;
+      const float code = static_cast<float>(
+          static_cast<int8_t>(static_cast<uint8_t>(packed >> (8 * i))));
+      const float a = s_shared[key] * code;
+      float d;
+      if constexpr (kFast) {
+        d = div_by_reciprocal(a, kQuantizedMaximum, kInvQuantizedMaximum);
       } else {
-        q = scale == 0.0f ? 0.0f : x[j][i] / scale;
+        d = a / kQuantizedMaximum;
       }
-      const int code = round_half_away_small(q * kQuantizedMaximum);
-      packed |= (static_cast<uint32_t>(code) & 0xFFu) << (8 * i);
+      float value_out = d * scale_shared[value];
+      if constexpr (kCompensated) {
+#pragma unroll
+        for (int r = 0; r < kRank; ++r) {
+          value_out += ck_shared[key * kRank + r] * cv_shared[value * kRank + r];
+        }
+      }
+      v[i] = value_out;
     }
-    *reinterpret_cast<uint32_t*>(out + (8 * j + group) * kDim + 4 * c4) =
-        packed;
+    store4(out + row * kDim + 4 * c4, v);
   }
 }
 
@@ -411,33 +478,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
 
   const int8_t* tile = codes + item * kTile;
   Out* out = dense + entry * kTile;
-#pragma unroll 4
-  for (int j = 0; j < kRowsPerThread; ++j) {
-    const int row = 8 * j + group;
-    const uint32_t packed =
-        *reinterpret_cast<const uint32_t*>(tile + row * kDim + 4 * c4);
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = kLayout == kKeyValue ? row : 4 * c4 + i;
-      const int value = kLayout == kKeyValue ? 4 * c4 + i : row;
-      const float code = static_cast<float>(
-          static_cast<int8_t>(static_cast<uint8_t>(packed >> (8 * i))));
-      const float a = s_shared[key] * code;
-      const float d = fast_divide
-                          ? div_by_reciprocal(a, kQuantizedMaximum,
-                                              kInvQuantizedMaximum)
-                          : a / kQuantizedMaximum;
-      float value_out = d * scale_shared[value];
-      if constexpr (kCompensated) {
-#pragma unroll
-        for (int r = 0; r < kRank; ++r) {
-          value_out += ck_shared[key * kRank + r] * cv_shared[value * kRank + r];
-        }
-      }
-      v[i] = value_out;
-    }
-    store4(out + row * kDim + 4 * c4, v);
+  if (fast_divide) {
+    decode_rows<kLayout, true, kCompensated>(tile, s_shared, scale_shared,
+                                             ck_shared, cv_shared, group, c4,
+                                             out);
+  } else {
+    decode_rows<kLayout, false, kCompensated>(tile, s_shared, scale_shared,
+                                              ck_shared, cv_shared, group, c4,
+                                              out);
   }
 }
 

@@ -16,7 +16,7 @@
 // converted in registers and accumulated with fp32 FMAs.
 //
 // Chunked (T queries per tile) is a [T x 128] x [128 x 128] contraction per
-// tile on bf16 MFMA (v_mfma_f32_32x32x16_bf16).  Codes are exact in bf16; the
+// tile on bf16 MFMA (v_mfma_f32_16x16x32_bf16).  Codes are exact in bf16; the
 // fp32 operand w[t][k] = s[k] * x_t[k] is split into three bf16 parts
 // w = hi + mid + lo (exact), staged in LDS in the MFMA operand order, so the
 // products are exact and only fp32 accumulation rounds.  The scale[v] / 127
@@ -26,6 +26,7 @@
 
 #include "codec_math.h"
 #include "launch.h"
+#include "stream_memory.h"
 
 namespace gdn {
 namespace {
@@ -75,7 +76,8 @@ __device__ __forceinline__ void reduce16_over_8_lanes(float (&p)[16], int lane,
 }
 
 template <uint32_t kLayout>
-__global__ __launch_bounds__(kThreads) void decode_projection_kernel(
+// 64 VGPRs: all 8192 wavefronts of a B=256, 32-head batch are resident at once.
+__global__ __launch_bounds__(kThreads, 8) void decode_projection_kernel(
     const int8_t* __restrict__ codes, const float* __restrict__ smoothing,
     const float* __restrict__ scales, const uint16_t* __restrict__ queries,
     float* __restrict__ out, uint64_t tiles, uint32_t value_heads,
@@ -100,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void decode_projection_kernel(
     uint4 row[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      row[j] = *reinterpret_cast<const uint4*>(c + (r8 + 8 * j) * kDim + 16 * kq);
+      row[j] = stream_load(reinterpret_cast<const uint4*>(c + (r8 + 8 * j) * kDim + 16 * kq));
     }
     float w[16];
 #pragma unroll
@@ -127,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void decode_projection_kernel(
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int v = r8 + 8 * (2 * kq + e);
-      o[v] = acc[e] / kQuantizedMaximum * scale[v];
+      stream_store(o + v, acc[e] / kQuantizedMaximum * scale[v]);
     }
   } else {
     // [key][value] codes: lane owns values 16*vc..+15 of key rows kr + 8j.
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void decode_projection_kernel(
     uint4 row[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      row[j] = *reinterpret_cast<const uint4*>(c + (kr + 8 * j) * kDim + 16 * vc);
+      row[j] = stream_load(reinterpret_cast<const uint4*>(c + (kr + 8 * j) * kDim + 16 * vc));
     }
     float w[16];
 #pragma unroll
@@ -159,23 +161,31 @@ __global__ __launch_bounds__(kThreads) void decode_projection_kernel(
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int v = 16 * vc + 2 * kr + e;
-      o[v] = acc[e] / kQuantizedMaximum * scale[v];
+      stream_store(o + v, acc[e] / kQuantizedMaximum * scale[v]);
     }
   }
 }
 
 // ----------------------------------------------------------------- chunked
 
-// bf16 split of an fp32 value into three round-to-nearest-even parts whose
-// sum is the value (each remainder is exact in fp32 and needs at most 8 more
-// significant bits).
-__device__ __forceinline__ void split3(float w, uint16_t& hi, uint16_t& mid,
-                                       uint16_t& lo) {
-  hi = float_to_bf16(w);
-  const float r1 = w - bf16_to_float(hi);
-  mid = float_to_bf16(r1);
-  const float r2 = r1 - bf16_to_float(mid);
-  lo = float_to_bf16(r2);
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+// Three-way bf16 split of a pair of fp32 values: w = hi + mid + lo, each part
+// rounded to nearest even by v_cvt_pk_bf16_f32; the remainders w - hi and
+// (w - hi) - mid are exact in fp32, so the parts carry all 24 significand bits.
+__device__ __forceinline__ void split3_pair(float w0, float w1, uint32_t& hi,
+                                            uint32_t& mid, uint32_t& lo) {
+  const bf16x2 h = {static_cast<__bf16>(w0), static_cast<__bf16>(w1)};
+  const float r0 = w0 - static_cast<float>(h[0]);
+  const float r1 = w1 - static_cast<float>(h[1]);
+  const bf16x2 m = {static_cast<__bf16>(r0), static_cast<__bf16>(r1)};
+  const float t0 = r0 - static_cast<float>(m[0]);
+  const float t1 = r1 - static_cast<float>(m[1]);
+  const bf16x2 l = {static_cast<__bf16>(t0), static_cast<__bf16>(t1)};
+  hi = __builtin_bit_cast(uint32_t, h);
+  mid = __builtin_bit_cast(uint32_t, m);
+  lo = __builtin_bit_cast(uint32_t, l);
 }
 
 __device__ __forceinline__ uint32_t pack_bf16_of_codes(uint32_t word, int pair) {
@@ -185,18 +195,37 @@ __device__ __forceinline__ uint32_t pack_bf16_of_codes(uint32_t word, int pair) 
   return (a >> 16) | (b & 0xFFFF0000u);
 }
 
-// Logical key order of the MFMA operands: for k-step s (0..7) and lane half g
-// (lane / 32), the 8 operand elements are keys 64g + 8s + i.  A (queries) and
-// B (codes) use the same order, so the contraction covers every key once, and
-// each lane's codes for all 8 steps are one contiguous 64-byte run.
+__device__ __forceinline__ bf16x8 codes_to_bf16x8(uint32_t w0, uint32_t w1) {
+  uint4 packed;
+  packed.x = pack_bf16_of_codes(w0, 0);
+  packed.y = pack_bf16_of_codes(w0, 1);
+  packed.z = pack_bf16_of_codes(w1, 0);
+  packed.w = pack_bf16_of_codes(w1, 1);
+  return __builtin_bit_cast(bf16x8, packed);
+}
+
+// v_mfma_f32_16x16x32_bf16 operands: lane l holds row (A) or column (B)
+// l % 16 and 8 consecutive elements of the contraction; the accumulator lane l
+// holds column l % 16, rows 4 * (l / 16) + r.  The logical key order used for
+// both operands is: k-step s (0..3), lane group g = l / 16 (0..3), element i
+// -> key 32g + 8s + i, so a lane's codes for all four steps are one contiguous
+// 32-byte run and the contraction covers every key exactly once.
+//
+// A workgroup owns one (sequence, head) tile; wavefront w owns the 32 values
+// 32w..32w+31 (two 16-column MFMA tiles) and keeps their codes in registers as
+// bf16 for every token block.  Token blocks of 16 rows are staged in LDS as the
+// three bf16 parts of w[t][k] = s[k] * x_t[k] in operand order (12 KiB), so
+// all 2048 workgroups of a 64 x 32-head batch are resident at once.
+// The [value][key] form fits 64 VGPRs (8 wavefronts per SIMD); the byte gathers
+// of the [key][value] form need more.
 template <uint32_t kLayout>
-__global__ __launch_bounds__(kThreads) void chunked_projection_kernel(
+__global__ __launch_bounds__(kThreads, kLayout == kValueKey ? 8 : 4) void chunked_projection_kernel(
     const int8_t* __restrict__ codes, const float* __restrict__ smoothing,
     const float* __restrict__ scales, const uint16_t* __restrict__ queries,
     float* __restrict__ out, uint32_t tokens, uint32_t value_heads,
     uint32_t group, uint32_t query_heads, float query_scale) {
-  // A operand, [split][k-step][lane] x 8 bf16 (16 B): 24 KiB.
-  __shared__ uint4 a_lds[3][8][64];
+  constexpr int kBlockTokens = 16;
+  __shared__ uint4 a_lds[3][4][64];  // [split][k-step][lane] x 8 bf16
   __shared__ float s_lds[kDim];
 
   const uint64_t pair = blockIdx.x;  // sequence * value_heads + head
@@ -206,114 +235,104 @@ __global__ __launch_bounds__(kThreads) void chunked_projection_kernel(
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
-  const int g = lane >> 5;
-  const int v = 32 * wave + (lane & 31);
+  const int col = lane & 15;
+  const int g = lane >> 4;
 
-  // B operand: codes(v, 64g + 8s + i) as bf16, s = 0..7.
-  bf16x8 b[8];
+  // B operands: for column tile c (0, 1) value v = 32 wave + 16 c + col and
+  // keys 32g + 8s + i, s = 0..3.
+  bf16x8 b[2][4];
   const int8_t* tile = codes + pair * kTile;
-  if constexpr (kLayout == kValueKey) {
-    const int8_t* run = tile + v * kDim + 64 * g;
 #pragma unroll
-    for (int part = 0; part < 4; ++part) {
-      const uint4 word4 = *reinterpret_cast<const uint4*>(run + 16 * part);
+  for (int c = 0; c < 2; ++c) {
+    const int v = 32 * wave + 16 * c + col;
+    if constexpr (kLayout == kValueKey) {
+      const int8_t* run = tile + v * kDim + 32 * g;
+      const uint4 lo = stream_load(reinterpret_cast<const uint4*>(run));
+      const uint4 hi = stream_load(reinterpret_cast<const uint4*>(run + 16));
+      b[c][0] = codes_to_bf16x8(lo.x, lo.y);
+      b[c][1] = codes_to_bf16x8(lo.z, lo.w);
+      b[c][2] = codes_to_bf16x8(hi.x, hi.y);
+      b[c][3] = codes_to_bf16x8(hi.z, hi.w);
+    } else {
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const uint32_t w0 = word_of(word4, 2 * half);
-        const uint32_t w1 = word_of(word4, 2 * half + 1);
-        uint4 packed;
-        packed.x = pack_bf16_of_codes(w0, 0);
-        packed.y = pack_bf16_of_codes(w0, 1);
-        packed.z = pack_bf16_of_codes(w1, 0);
-        packed.w = pack_bf16_of_codes(w1, 1);
-        b[2 * part + half] = __builtin_bit_cast(bf16x8, packed);
+      for (int step = 0; step < 4; ++step) {
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          w0 |= static_cast<uint32_t>(static_cast<uint8_t>(
+                    tile[(32 * g + 8 * step + i) * kDim + v]))
+                << (8 * i);
+          w1 |= static_cast<uint32_t>(static_cast<uint8_t>(
+                    tile[(32 * g + 8 * step + 4 + i) * kDim + v]))
+                << (8 * i);
+        }
+        b[c][step] = codes_to_bf16x8(w0, w1);
       }
-    }
-  } else {
-#pragma unroll
-    for (int step = 0; step < 8; ++step) {
-      uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        w0 |= static_cast<uint32_t>(static_cast<uint8_t>(
-                  tile[(64 * g + 8 * step + i) * kDim + v]))
-              << (8 * i);
-        w1 |= static_cast<uint32_t>(static_cast<uint8_t>(
-                  tile[(64 * g + 8 * step + 4 + i) * kDim + v]))
-              << (8 * i);
-      }
-      uint4 packed;
-      packed.x = pack_bf16_of_codes(w0, 0);
-      packed.y = pack_bf16_of_codes(w0, 1);
-      packed.z = pack_bf16_of_codes(w1, 0);
-      packed.w = pack_bf16_of_codes(w1, 1);
-      b[step] = __builtin_bit_cast(bf16x8, packed);
     }
   }
-  const float epilogue = scales[pair * kDim + v] / kQuantizedMaximum;
+  float epilogue[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    epilogue[c] = scales[pair * kDim + 32 * wave + 16 * c + col] / kQuantizedMaximum;
+  }
   if (t < kDim) s_lds[t] = smoothing[pair * kDim + t];
 
-  // Producer role: thread t builds w for token row m = t / 8 of the block and
-  // keys 16*kc..+15, which are k-steps 2*(kc%4) + {0,1} of lane half kc / 4.
-  const int m = t >> 3;
-  const int kc = t & 7;
-  const int dst_lane = m + 32 * (kc >> 2);
-  const int dst_step = 2 * (kc & 3);
+  // Producer role: thread t builds token row m = t / 16 of the block, keys
+  // 8*kc..+7 (kc = t % 16), which is k-step kc % 4 of lane group kc / 4.
+  const int m = t >> 4;
+  const int kc = t & 15;
+  const int dst_lane = m + 16 * (kc >> 2);
+  const int dst_step = kc & 3;
 
-  for (uint32_t block = 0; block < tokens; block += 32) {
+  for (uint32_t block = 0; block < tokens; block += kBlockTokens) {
     __syncthreads();  // s_lds ready / previous block's operands consumed
     const uint32_t token = block + m;
-    uint32_t qw[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint4 qv = make_uint4(0, 0, 0, 0);
     if (token < tokens) {
-      const uint16_t* qrow =
-          queries + ((n * tokens + token) * query_heads + qh) * kDim + 16 * kc;
-      const uint4 q0 = *reinterpret_cast<const uint4*>(qrow);
-      const uint4 q1 = *reinterpret_cast<const uint4*>(qrow + 8);
-      qw[0] = q0.x; qw[1] = q0.y; qw[2] = q0.z; qw[3] = q0.w;
-      qw[4] = q1.x; qw[5] = q1.y; qw[6] = q1.z; qw[7] = q1.w;
+      qv = *reinterpret_cast<const uint4*>(
+          queries + ((n * tokens + token) * query_heads + qh) * kDim + 8 * kc);
     }
+    const float4 s0 = *reinterpret_cast<const float4*>(s_lds + 8 * kc);
+    const float4 s1 = *reinterpret_cast<const float4*>(s_lds + 8 * kc + 4);
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    uint32_t hi[4], mid[4], lo[4];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      uint32_t hi[4], mid[4], lo[4];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        uint16_t h2[2], m2[2], l2[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int i = 8 * half + 2 * p + e;  // 0..15 within the chunk
-          const uint16_t qbits = static_cast<uint16_t>(qw[i >> 1] >> (16 * (i & 1)));
-          const float x = query_scale * bf16_to_float(qbits);
-          const float w = s_lds[16 * kc + i] * x;
-          split3(w, h2[e], m2[e], l2[e]);
-        }
-        hi[p] = h2[0] | (static_cast<uint32_t>(h2[1]) << 16);
-        mid[p] = m2[0] | (static_cast<uint32_t>(m2[1]) << 16);
-        lo[p] = l2[0] | (static_cast<uint32_t>(l2[1]) << 16);
-      }
-      a_lds[0][dst_step + half][dst_lane] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-      a_lds[1][dst_step + half][dst_lane] = make_uint4(mid[0], mid[1], mid[2], mid[3]);
-      a_lds[2][dst_step + half][dst_lane] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t word = word_of(qv, p);
+      const float w0 = sv[2 * p] * (query_scale * bf16_to_float(word & 0xFFFFu));
+      const float w1 = sv[2 * p + 1] * (query_scale * bf16_to_float(word >> 16));
+      split3_pair(w0, w1, hi[p], mid[p], lo[p]);
     }
+    a_lds[0][dst_step][dst_lane] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    a_lds[1][dst_step][dst_lane] = make_uint4(mid[0], mid[1], mid[2], mid[3]);
+    a_lds[2][dst_step][dst_lane] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
     __syncthreads();
 
-    f32x16 acc;
+    f32x4 acc[2];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    for (int c = 0; c < 2; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int step = 0; step < 8; ++step) {
+    for (int step = 0; step < 4; ++step) {
 #pragma unroll
       for (int split = 0; split < 3; ++split) {
         const bf16x8 a = __builtin_bit_cast(bf16x8, a_lds[split][step][lane]);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[step], acc, 0, 0, 0);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[c][step], acc[c],
+                                                           0, 0, 0);
+        }
       }
     }
-    // Accumulator element r of lane holds row 8*(r/4) + 4*g + r%4, column v.
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const uint32_t row_token = block + 8 * (r >> 2) + 4 * g + (r & 3);
-      if (row_token < tokens) {
-        out[((n * tokens + row_token) * value_heads + h) * kDim + v] =
-            acc[r] * epilogue;
+    for (int c = 0; c < 2; ++c) {
+      const int v = 32 * wave + 16 * c + col;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t row_token = block + 4 * g + r;
+        if (row_token < tokens) {
+          stream_store(out + ((n * tokens + row_token) * value_heads + h) * kDim + v,
+                       acc[c][r] * epilogue[c]);
+        }
       }
     }
   }

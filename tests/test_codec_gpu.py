@@ -201,7 +201,9 @@ def test_encode_is_deterministic_and_leaves_input_untouched(device):
 def test_full_config2_shape_properties(device):
     """BASELINE config 2 at full size ([30,256,32,128,128] fp32): codes within
     +-127, every live column reaches 127, round-trip error within half a code
-    step, and 64 sampled heads bit-exact against the oracle."""
+    step s*scale/127 (plus 2e-4 of it for the six fp32 roundings of the
+    encode/decode chain, at most 6 * 127 * 2^-24 of a step), and 64 sampled
+    heads bit-exact against the oracle."""
     print("full config-2 properties", flush=True)
     shape = (30, 256, 32, 128, 128)
     gen = torch.Generator(device=device)
@@ -222,7 +224,7 @@ def test_full_config2_shape_properties(device):
         assert bool(((live_max == 127) | (flat_sc[rows] == 0)).all())
         step = flat_s[rows].view(-1, 128, 1) * flat_sc[rows].view(-1, 1, 128) / 127
         err = (dense.view(-1, 128, 128)[rows] - state.view(-1, 128, 128)[rows]).abs_()
-        assert bool((err <= 0.5 * step * (1 + 1e-5) + 1e-30).all()), layer
+        assert bool((err <= 0.5 * step * (1 + 2e-4) + 1e-30).all()), layer
         del step, err, live_max
     idx = torch.randint(0, flat_codes.shape[0], (64,), generator=gen, device=device)
     sample = state.view(-1, 128, 128)[idx].cpu().numpy()
