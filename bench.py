@@ -234,8 +234,15 @@ def bench_pool(steps: int, warmup: int):
     layers, slots, heads, batch = 30, 2048, 32, 512
     pool = torch.empty((layers, slots, heads, 128, 128), dtype=torch.bfloat16, device=dev)
     for layer in range(layers):
-        t = torch.distributions.StudentT(torch.tensor(3.0, device=dev))
-        pool[layer] = (t.sample((slots, heads, 128, 128)) * 0.05).to(torch.bfloat16)
+        # Student-t(3) = Z / sqrt(chi2_3 / 3), chi2_3 a sum of three squared normals.
+        for part in range(0, slots, 256):
+            shape = (min(256, slots - part), heads, 128, 128)
+            z = torch.randn(shape, generator=gen, device=dev)
+            chi = torch.zeros(shape, device=dev)
+            for _ in range(3):
+                chi.addcmul_(w := torch.randn(shape, generator=gen, device=dev), w)
+            pool[layer, part:part + shape[0]] = (z * torch.rsqrt(chi / 3) * 0.05).to(torch.bfloat16)
+            del z, chi, w
     zero = torch.rand((layers, slots, heads), generator=gen, device=dev) < 0.02
     pool[zero] = 0
     perm = torch.randperm(slots, generator=gen, device=dev)[:batch].to(torch.int32)

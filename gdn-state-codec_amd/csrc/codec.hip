@@ -234,11 +234,17 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   bool fast_divide = false;
   if constexpr (kMode != kModeGivenSmoothing) {
     // ---- smoothing: per-key double sums of |r| ------------------------------
-    float min_abs = fabsf(x[0][0]);
+    // min_abs is the smallest NON-ZERO |r|: zeros add nothing to a key sum and
+    // divide exactly on both division paths, so they must not force the slow
+    // paths (dequantized states hold many exact zeros, one per code 0).
+    float min_abs = INFINITY;
 #pragma unroll
     for (int j = 0; j < kRowsPerThread; ++j) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) min_abs = fminf(min_abs, fabsf(x[j][i]));
+      for (int i = 0; i < 4; ++i) {
+        const float a = fabsf(x[j][i]);
+        min_abs = fminf(min_abs, a == 0.0f ? INFINITY : a);
+      }
     }
     if constexpr (kLayout == kKeyValue) {
       double p[kRowsPerThread];
@@ -274,8 +280,10 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
     }
     __syncthreads();
 
-    // Tile-wide smallest |r| and largest key sum decide whether the tree sums
-    // are exact.
+    // Tile-wide smallest non-zero |r| and largest key sum decide whether the
+    // tree sums are exact: every non-zero |r| >= 2^e is a multiple of
+    // 2^(e-23), so every partial sum below 2^(e+29) is a double without
+    // rounding and any summation order gives the sequential sum.
     double tmax = t < kDim ? key_sum[t] : 0.0;
     for (int mask = 32; mask >= 1; mask >>= 1) {
       min_abs = fminf(min_abs, __shfl_xor(min_abs, mask));
@@ -291,7 +299,7 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
     tmax = fmax(fmax(tmax_part[0], tmax_part[1]),
                 fmax(tmax_part[2], tmax_part[3]));
     bool exact = tmax == 0.0;
-    if (!exact && min_abs > 0.0f) {
+    if (!exact && min_abs < INFINITY) {
       const int e = granularity_exponent(min_abs) + 29;
       const double bound =
           __longlong_as_double(static_cast<long long>(e + 1023) << 52);
@@ -309,9 +317,11 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
       smoothing[item * kDim + t] = s;
     }
     if constexpr (kMode == kModeSmoothingOnly) return;
-    // Markstein division is exact for every r / s when the smallest |r| is at
-    // least 2^-100 and s <= 2^20 (key sums <= 2^46): |r/s| <= 128 s stays far
-    // from overflow and >= 2^-120 stays normal.
+    // Markstein division is exact for every r / s when the smallest non-zero
+    // |r| is at least 2^-100 and s <= 2^20 (key sums <= 2^46): |r/s| <= 128 s
+    // stays far from overflow and >= 2^-120 stays normal.  r = +-0 gives +0
+    // where IEEE gives +-0; m only feeds max |m| and lround(m / scale * 127),
+    // neither of which sees the sign of a zero.
     fast_divide = min_abs >= 0x1p-100f && tmax <= 0x1p46;
   } else {
     if (t < kDim) {

@@ -153,7 +153,7 @@ def test_config1_round_trip_matches_reference_digests(device):
 
 
 @pytest.mark.parametrize("layout", [KV, VK])
-@pytest.mark.parametrize("kind", ["c1", "student_t", "wide", "tiny_and_huge"])
+@pytest.mark.parametrize("kind", ["c1", "student_t", "wide", "tiny_and_huge", "requantize"])
 def test_encode_decode_match_oracle_on_random_heads(device, layout, kind):
     print(f"random parity layout={layout} kind={kind}", flush=True)
     if kind == "c1":
@@ -162,9 +162,17 @@ def test_encode_decode_match_oracle_on_random_heads(device, layout, kind):
         x = datagen.student_t_heads(384, 6, zero_fraction=0.02)
     elif kind == "wide":
         x = np.stack([datagen.wide_range_head(100 + i) for i in range(48)])
-    else:
+    elif kind == "tiny_and_huge":
         x = np.stack([datagen.tiny_head(200 + i) for i in range(24)]
                      + [datagen.huge_head(300 + i) for i in range(24)])
+    else:
+        # A window boundary re-encodes dequantized states: every code 0 became
+        # an exact zero.  Half of those zeros are made -0.
+        x = datagen.student_t_heads(256, 7)
+        x = oracle.decode_heads(*oracle.encode_heads(x, layout, threads=8), layout, threads=8)
+        zeros = np.flatnonzero(x == 0)
+        assert zeros.size > 0
+        x.reshape(-1)[zeros[::2]] = -0.0
     codes, s, sc = oracle.encode_heads(x, layout, threads=8)
     c_gpu, s_gpu, sc_gpu = codec.encode(to_gpu(x, device), layout)
     assert to_np(c_gpu).tobytes() == codes.tobytes()
