@@ -131,6 +131,139 @@ void gdn_oracle_pool_decode(const int8_t* codes, const float* smoothing,
 float gdn_oracle_bf16_to_f32(uint16_t value);
 uint16_t gdn_oracle_f32_to_bf16(float value);
 
+/* fp16 helpers (IEEE binary16): widening is exact; narrowing rounds to nearest
+ * even with subnormals and overflow to infinity. */
+float gdn_oracle_f16_to_f32(uint16_t value);
+uint16_t gdn_oracle_f32_to_f16(float value);
+
+/* ---- windowed decode step (gdn_window_oracle.c) ---------------------------
+ *
+ * Parity pins:
+ *   read_window / dense_state / apply_token : bit-exact vs oracle/_ref, which
+ *        drives the reference capsule (ApplyToken over whole windows, rank 0
+ *        and rank 4, including the window-boundary requantize).
+ *   windowed_step_{bf16,f16}, gdn_step_f32 : built from read_window plus the
+ *        device kernels' input conventions; checked against the dense fp32 GDN
+ *        step on the reconstructed state (the reference probe's own check,
+ *        windowed_gdn_runtime_probe.cpp:94-147, here to 2^-14 of the error
+ *        scale instead of 0.25% RMS) and against their own double results.
+ *   decode-pair chain : the reference kernels' scalar fp32 code restated
+ *        statement by statement; the chain is checked end to end against
+ *        windowed_step_* within its documented int8 vector quantization error.
+ * Every device entry point takes g = RN_fp32(exp(log_decay)) (evaluated as
+ * (float)exp((double)x)) where the reference evaluates Ascend's Exp. */
+
+/* ReadWindowState (state_capsule.cpp:253-306): [key][value] boundary, records
+ * u = 0..records-1 with per-key decay [records][keys], key [records][keys] and
+ * correction [records][values]; output[v] = S^T read. */
+void gdn_oracle_read_window(const int8_t* codes, const float* smoothing,
+                            const float* value_scales, const float* comp_keys,
+                            const float* comp_values, uint32_t keys,
+                            uint32_t values, uint32_t rank,
+                            const float* record_decay, const float* record_keys,
+                            const float* record_corrections, uint32_t records,
+                            const float* read, float* output);
+
+/* DenseState (state_capsule.cpp:337-352). */
+void gdn_oracle_dense_state(const int8_t* codes, const float* smoothing,
+                            const float* value_scales, const float* comp_keys,
+                            const float* comp_values, uint32_t keys,
+                            uint32_t values, uint32_t rank,
+                            const float* record_decay, const float* record_keys,
+                            const float* record_corrections, uint32_t records,
+                            float* state);
+
+/* ApplyToken (state_capsule.cpp:354-397).  The boundary arrays are replaced in
+ * place when the window fills (DenseState then QuantizeBoundary at the same
+ * rank); record arrays hold `window` rows; *records is the window position.
+ * Returns 1 when the token crossed the window boundary. */
+int gdn_oracle_apply_token(int8_t* codes, float* smoothing, float* value_scales,
+                           float* comp_keys, float* comp_values, uint32_t keys,
+                           uint32_t values, uint32_t rank, uint32_t window,
+                           float* record_decay, float* record_keys,
+                           float* record_corrections, uint32_t* records,
+                           const float* decay, const float* key,
+                           const float* value, const float* read,
+                           const float* query, float* output);
+
+/* windowed_gdn_step_bf16{,_quant_only}_launch_v1 on device buffers
+ * (kernel/gdn_state_codec_windowed_gdn_step.cpp:326-619, 720-775).
+ * residual [S][value][key] int8; comp_keys [S][key][4] / comp_values
+ * [S][value][4] fp16, both NULL for the quant-only form; record_decay [S][16]
+ * fp32; record_keys / record_corrections [S][16][128] fp16; positions [S][8];
+ * log_decay fp32 [S]; beta bf16 [S]; keys / queries bf16 [S/2][128] (value head
+ * h reads head h/2); values / outputs bf16 [S][128].  With g = exp(log_decay),
+ * key k, q = 0.08838834764831845 * query:
+ *   read = g*k, output vector = q*g, write key = beta*k,
+ *   correction = value - S^T read, out = S^T (q*g) + correction * (beta*k . q),
+ * then record p = {g, fp16(beta*k), fp16(correction)} and position p+1.
+ * States at position >= 16 are untouched.  out64 / corr64 (nullable) receive
+ * the output and correction before rounding, in double, and out_bound /
+ * corr_bound the magnitude their fp32 evaluation error scales with. */
+void gdn_oracle_windowed_step_bf16(
+    const int8_t* residual, const float* smoothing, const float* scales,
+    const uint16_t* comp_keys, const uint16_t* comp_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    const float* log_decay, const uint16_t* beta, const uint16_t* keys,
+    const uint16_t* queries, const uint16_t* values, uint16_t* outputs,
+    uint32_t states, double* out64, double* out_bound, double* corr64,
+    double* corr_bound);
+
+/* windowed_gdn_step_launch_v1 (windowed_gdn_step.cpp:34-187, 667-688):
+ * residual [S][key][value]; fp16 write_keys / reads / queries / values
+ * [S][128]; linear decay fp32 [S]; fp32 outputs; fp16 rank-4 compensators.
+ *   correction = value - S^T read, out = S^T (query*decay) + correction *
+ *   (write_key . query); record p = {decay, write_key, fp16(correction)}. */
+void gdn_oracle_windowed_step_f16(
+    const int8_t* residual, const float* smoothing, const float* scales,
+    const uint16_t* comp_keys, const uint16_t* comp_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    const float* decay, const uint16_t* write_keys, const uint16_t* reads,
+    const uint16_t* queries, const uint16_t* values, float* outputs,
+    uint32_t states, double* out64, double* out_bound, double* corr64,
+    double* corr_bound);
+
+/* fp32_gdn_step_launch_v1 (kernel/gdn_state_codec_fp32_gdn_step.cpp:13-18):
+ * dense [S][key][value] fp32 state updated in place. */
+void gdn_oracle_gdn_step_f32(float* state, const float* decay,
+                             const uint16_t* keys, const uint16_t* reads,
+                             const uint16_t* queries, const uint16_t* values,
+                             float* outputs, uint32_t states);
+
+/* The cube decode chain (kernel/gdn_state_codec_encoded_projection.cpp and
+ * int8_cube_matmul.cpp), statement by statement: quantized [S][128][16] int8
+ * (columns hi0, lo0, hi1, lo1, then zeros), dynamic_scale [S][8] (hi0, hi1,
+ * lo0, lo1), projected [S][128][16] int32. */
+void gdn_oracle_prepare_decode_pair_bf16(const uint16_t* keys,
+                                         const uint16_t* queries,
+                                         const float* log_decay,
+                                         const float* smoothing,
+                                         int8_t* quantized, float* dynamic_scale,
+                                         uint32_t states);
+void gdn_oracle_prepare_decode_pair(const uint16_t* reads, const uint16_t* queries,
+                                    const float* decay, const float* smoothing,
+                                    int8_t* quantized, float* dynamic_scale,
+                                    uint32_t states);
+void gdn_oracle_prepare_int8_vector(const uint16_t* input, const float* axis_scale,
+                                    int8_t* quantized, float* dynamic_scale,
+                                    uint32_t states);
+void gdn_oracle_int8_matmul(const int8_t* a, const int8_t* b, int32_t* c,
+                            uint32_t states, uint32_t transpose_a);
+void gdn_oracle_finish_decode_pair_bf16(
+    const int32_t* projected, const float* dynamic_scale, const float* scales,
+    const uint16_t* comp_keys, const uint16_t* comp_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    const float* log_decay, const uint16_t* beta, const uint16_t* keys,
+    const uint16_t* queries, const uint16_t* values, uint16_t* outputs,
+    uint32_t states);
+void gdn_oracle_finish_decode_pair(
+    const int32_t* projected, const float* dynamic_scale, const float* scales,
+    const uint16_t* comp_keys, const uint16_t* comp_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    const float* decay, const uint16_t* write_keys, const uint16_t* reads,
+    const uint16_t* queries, const uint16_t* values, float* outputs,
+    uint32_t states);
+
 #ifdef __cplusplus
 }
 #endif

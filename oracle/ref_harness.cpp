@@ -154,6 +154,85 @@ int gdnref_codec_to_provider(const float* codec, std::uint32_t keys,
   }
 }
 
+// ReadWindowState with `records` buffered updates (state_capsule.cpp:253-306):
+// record u has per-key decay [keys], key [keys] and correction [values].
+int gdnref_read_window(const std::int8_t* residual, const float* smoothing,
+                       const float* value_scales, const float* compensator_keys,
+                       const float* compensator_values, std::uint32_t keys,
+                       std::uint32_t values, std::uint32_t rank,
+                       const float* record_decay, const float* record_keys,
+                       const float* record_corrections, std::uint32_t records,
+                       const float* read, float* output) {
+  try {
+    const auto identity = MakeIdentity(keys, values);
+    const auto parameters = MakeParameters(rank);
+    statecentric::GdnStateCodecCapsule::Boundary boundary;
+    boundary.residual.assign(residual, residual + std::size_t{keys} * values);
+    boundary.smoothing.assign(smoothing, smoothing + keys);
+    boundary.value_scales.assign(value_scales, value_scales + values);
+    if (rank > 0) {
+      boundary.compensator_keys.assign(
+          compensator_keys, compensator_keys + std::size_t{keys} * rank);
+      boundary.compensator_values.assign(
+          compensator_values, compensator_values + std::size_t{values} * rank);
+    }
+    std::vector<statecentric::GdnStateCodecCapsule::UpdateRecord> updates(records);
+    for (std::uint32_t u = 0; u < records; ++u) {
+      updates[u].decay.assign(record_decay + std::size_t{u} * keys,
+                              record_decay + std::size_t{u + 1} * keys);
+      updates[u].key.assign(record_keys + std::size_t{u} * keys,
+                            record_keys + std::size_t{u + 1} * keys);
+      updates[u].correction.assign(record_corrections + std::size_t{u} * values,
+                                   record_corrections + std::size_t{u + 1} * values);
+    }
+    const auto out = statecentric::ReadWindowState(
+        boundary, updates, std::span<const float>(read, keys), identity,
+        parameters);
+    std::memcpy(output, out.data(), out.size() * sizeof(float));
+    return 0;
+  } catch (const std::exception&) {
+    return 1;
+  }
+}
+
+// The reference capsule stepped through `tokens` tokens: FromDenseBoundary at
+// compensator_rank = rank (window 16; the public capsule admits rank 4
+// only, state_capsule.cpp:26-38), then ApplyToken per token
+// (state_capsule.cpp:318-335, 354-397).  Token inputs are [tokens][keys]
+// (decay, key, read, query) and [tokens][values] (value); outputs
+// [tokens][values], crossed[t] = 1 when token t refit the boundary, and
+// final_dense = DenseState() after the last token.
+int gdnref_apply_tokens(const float* dense, std::uint32_t keys,
+                        std::uint32_t values, std::uint32_t rank,
+                        std::uint32_t tokens, const float* decay,
+                        const float* key, const float* value, const float* read,
+                        const float* query, float* outputs,
+                        std::uint8_t* crossed, float* final_dense) {
+  try {
+    auto capsule = statecentric::GdnStateCodecCapsule::FromDenseBoundary(
+        std::span<const float>(dense, std::size_t{keys} * values),
+        MakeIdentity(keys, values), MakeParameters(rank));
+    for (std::uint32_t t = 0; t < tokens; ++t) {
+      statecentric::GdnStateCodecTokenInput input;
+      input.decay.assign(decay + std::size_t{t} * keys, decay + std::size_t{t + 1} * keys);
+      input.key.assign(key + std::size_t{t} * keys, key + std::size_t{t + 1} * keys);
+      input.read.assign(read + std::size_t{t} * keys, read + std::size_t{t + 1} * keys);
+      input.query.assign(query + std::size_t{t} * keys, query + std::size_t{t + 1} * keys);
+      input.value.assign(value + std::size_t{t} * values,
+                         value + std::size_t{t + 1} * values);
+      const auto result = capsule.ApplyToken(input);
+      std::memcpy(outputs + std::size_t{t} * values, result.output.data(),
+                  values * sizeof(float));
+      crossed[t] = result.crossed_window_boundary ? 1 : 0;
+    }
+    const auto state = capsule.DenseState();
+    std::memcpy(final_dense, state.data(), state.size() * sizeof(float));
+    return 0;
+  } catch (const std::exception&) {
+    return 1;
+  }
+}
+
 // Batched quant-only encode over `heads` contiguous [K][V] tiles, used as the
 // reference CPU baseline (single thread, the reference's own code).
 int gdnref_quantize_heads(const float* dense, std::uint64_t heads,
