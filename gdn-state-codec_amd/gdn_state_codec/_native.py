@@ -43,6 +43,25 @@ SIGNATURES: dict[str, list] = {
         _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _F, _U32],
     "statecentric_gdn_state_codec_encoded_projection_chunked_launch_v4": [
         _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _F, _U32],
+    # windowed decode step (include/gdn_state_codec_window.h)
+    "statecentric_gdn_state_codec_windowed_gdn_step_launch_v1": [_P] * 16 + [_U32],
+    "statecentric_gdn_state_codec_windowed_gdn_step_bf16_launch_v1": [_P] * 16 + [_U32],
+    "statecentric_gdn_state_codec_windowed_gdn_step_bf16_quant_only_launch_v1": [_P] * 16 + [_U32],
+    "statecentric_gdn_state_codec_fp32_gdn_step_launch_v1": [_P] * 8 + [_U32],
+    "statecentric_gdn_state_codec_prepare_int8_vector_launch_v1": [_P] * 5 + [_U32],
+    "statecentric_gdn_state_codec_prepare_decode_pair_launch_v1": [_P] * 7 + [_U32],
+    "statecentric_gdn_state_codec_prepare_decode_pair_bf16_launch_v1": [_P] * 7 + [_U32],
+    "statecentric_gdn_state_codec_finish_decode_pair_launch_v1": [_P] * 16 + [_U32],
+    "statecentric_gdn_state_codec_finish_decode_pair_bf16_launch_v1": [_P] * 16 + [_U32],
+    "statecentric_gdn_state_codec_int8_cube_matmul_launch_v1": [
+        _P, _P, _P, _P, _U32, _U32, _P, _P, _U32],
+    "statecentric_gdn_state_codec_decode_runtime_step_v1": [_P] * 17 + [_U32],
+}
+
+# Entry points that do not return a status: name -> (argtypes, restype).
+OTHER_SIGNATURES: dict[str, tuple] = {
+    "statecentric_gdn_state_codec_decode_runtime_create_v1": ([_U32], _P),
+    "statecentric_gdn_state_codec_decode_runtime_destroy_v1": ([_P], None),
 }
 
 
@@ -71,6 +90,11 @@ class NativeLibrary:
             fn = getattr(self._lib, name)
             fn.argtypes = argtypes
             fn.restype = _I32
+            setattr(self, name.removeprefix("statecentric_gdn_state_codec_"), fn)
+        for name, (argtypes, restype) in OTHER_SIGNATURES.items():
+            fn = getattr(self._lib, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
             setattr(self, name.removeprefix("statecentric_gdn_state_codec_"), fn)
 
     def symbol(self, name: str):

@@ -1,0 +1,174 @@
+/*
+ * C-ABI of the MI355X (gfx950) windowed GDN decode step: one token of the gated
+ * delta rule evaluated against the encoded state (int8 boundary, rank-4 fp16
+ * compensators and up to 15 buffered fp16 rank-one records) without
+ * materializing it, plus the reference's decode-pair chain and dense fp32
+ * step.  Same names, arguments, admission and status codes as the reference
+ * (native/include/statecentric/gdn_state_codec_windowed_gdn_kernel.h).
+ *
+ * Buffers (one "state" = one value head of one sequence):
+ *   residual        int8  [S][128][128]  [key][value] for the fp16 v1 step,
+ *                                         [value][key] for the bf16 steps and
+ *                                         the decode-pair chain
+ *   smoothing       fp32  [S][128] (by key)    scales fp32 [S][128] (by value)
+ *   compensator_keys fp16 [S][128][4]         compensator_values fp16 [S][128][4]
+ *   record_decay    fp32  [S][16]             record_keys / record_corrections
+ *                                              fp16 [S][16][128]
+ *   positions       uint32 [S][8]  (word 0 is the window position, 0..16; the
+ *                                   other words are never touched)
+ * A step on a state at position p < 16 reads records 0..p-1, writes record p
+ * and sets position p + 1; states at position >= 16 are left untouched (the
+ * boundary refit must run first).
+ *
+ * Semantics (native/src/gdn_state_codec_state_capsule.cpp:354-397 with the
+ * per-entry-point input mapping stated below): with S the encoded state,
+ *   correction = value - S^T read,  out = S^T (query*gate) + correction*(w.query)
+ * and the new record is {gate, w, fp16(correction)}.  All arithmetic is fp32;
+ * outputs are within 2^-14 of the double-precision result's error scale (sum
+ * of |terms|) before their final rounding -- tighter than the reference's
+ * Ascend kernels, which accumulate the boundary readout in fp16.
+ *
+ * Every entry point is asynchronous on `stream` (NULL = HIP's null stream) and
+ * returns 0 on success, 1 for a null pointer or an out-of-range count (the
+ * reference's status 1), 5 when HIP rejects a launch.
+ */
+#ifndef GDN_STATE_CODEC_WINDOW_H
+#define GDN_STATE_CODEC_WINDOW_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fp16 step, [key][value] residual, 1 <= states <= 16384.  write_keys, reads,
+ * queries, values fp16 [S][128]; decay fp32 [S] is the linear gate g.
+ * read = reads, query vector = queries*g, w = write_keys (stored as given),
+ * outputs fp32 [S][128].  Replaces windowed_gdn_kernel.h:8-16
+ * (kernel/gdn_state_codec_windowed_gdn_step.cpp:34-187, 667-688). */
+int32_t statecentric_gdn_state_codec_windowed_gdn_step_launch_v1(
+    void* stream, const int8_t* residual, const float* smoothing,
+    const float* scales, const uint16_t* compensator_keys,
+    const uint16_t* compensator_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    const float* decay, const uint16_t* write_keys, const uint16_t* reads,
+    const uint16_t* queries, const uint16_t* values, float* outputs,
+    uint32_t states);
+
+/* bf16 step for Qwen3.5 decode, [value][key] residual, even states in
+ * 1..16384.  decay fp32 [S] is log(g); beta bf16 [S]; keys and queries bf16
+ * [S/2][128] (value head h reads key/query head h/2); values and outputs bf16
+ * [S][128].  With k the key and q = 0.08838834764831845 * query:
+ * read = g*k, query vector = q*g, w = beta*k.  Replaces
+ * windowed_gdn_kernel.h:18-29 (windowed_gdn_step.cpp:189-619, 720-746). */
+int32_t statecentric_gdn_state_codec_windowed_gdn_step_bf16_launch_v1(
+    void* stream, const int8_t* residual, const float* smoothing,
+    const float* scales, const uint16_t* compensator_keys,
+    const uint16_t* compensator_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    const float* decay, const uint16_t* beta, const uint16_t* keys,
+    const uint16_t* queries, const uint16_t* values, uint16_t* outputs,
+    uint32_t states);
+
+/* The bf16 step of a quant-only boundary: as above without the compensator
+ * term (the compensator pointers are still required, as in the reference).
+ * Replaces windowed_gdn_kernel.h:31-40 (windowed_gdn_step.cpp:748-775). */
+int32_t statecentric_gdn_state_codec_windowed_gdn_step_bf16_quant_only_launch_v1(
+    void* stream, const int8_t* residual, const float* smoothing,
+    const float* scales, const uint16_t* compensator_keys,
+    const uint16_t* compensator_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    const float* decay, const uint16_t* beta, const uint16_t* keys,
+    const uint16_t* queries, const uint16_t* values, uint16_t* outputs,
+    uint32_t states);
+
+/* Dense fp32 GDN step on a [S][key][value] fp32 state, updated in place:
+ * per value column c, projection = sum_r S[r][c]*read[r], correction =
+ * value[c] - projection, S'[r][c] = decay*S[r][c] + key[r]*correction,
+ * out[c] = sum_r S'[r][c]*query[r] (sequential fp32 sums, bit-identical to the
+ * CPU statement of the reference kernel).  Replaces windowed_gdn_kernel.h:42-46
+ * (kernel/gdn_state_codec_fp32_gdn_step.cpp:1-23). */
+int32_t statecentric_gdn_state_codec_fp32_gdn_step_launch_v1(
+    void* stream, float* dense_state, const float* decay,
+    const uint16_t* write_keys, const uint16_t* reads, const uint16_t* queries,
+    const uint16_t* values, float* outputs, uint32_t states);
+
+/* ---- the reference's cube decode chain ------------------------------------
+ * quantized int8 [S][128][16]: column 2c / 2c+1 hold the high / low int8 code of
+ * vector c (c = 0: the read vector x s, c = 1: the output vector x s), columns
+ * 4..15 are zero; dynamic_scale fp32 [S][8] holds {hi0, hi1, lo0, lo1};
+ * projected int32 [S][128][16] = residual[value][key] x quantized (exact).
+ * Rounding adds +-0.5 and truncates, as the reference does.  These kernels are
+ * bit-identical to the reference's scalar code restated on the CPU. */
+
+/* Replaces windowed_gdn_kernel.h:113-115
+ * (kernel/gdn_state_codec_encoded_projection.cpp:179-234, 867-876). */
+int32_t statecentric_gdn_state_codec_prepare_int8_vector_launch_v1(
+    void* stream, const uint16_t* input, const float* axis_scale,
+    int8_t* quantized, float* dynamic_scale, uint32_t states);
+
+/* Replaces windowed_gdn_kernel.h:117-120 (encoded_projection.cpp:236-353, 878-890). */
+int32_t statecentric_gdn_state_codec_prepare_decode_pair_launch_v1(
+    void* stream, const uint16_t* reads, const uint16_t* queries,
+    const float* decay, const float* smoothing, int8_t* quantized,
+    float* dynamic_scale, uint32_t states);
+
+/* Replaces windowed_gdn_kernel.h:122-131 (encoded_projection.cpp:482-621, 892-918). */
+int32_t statecentric_gdn_state_codec_finish_decode_pair_launch_v1(
+    void* stream, const int32_t* projected, const float* dynamic_scale,
+    const float* scales, const uint16_t* compensator_keys,
+    const uint16_t* compensator_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    const float* decay, const uint16_t* write_keys, const uint16_t* reads,
+    const uint16_t* queries, const uint16_t* values, float* outputs,
+    uint32_t states);
+
+/* Replaces windowed_gdn_kernel.h:133-137 (encoded_projection.cpp:355-479, 920-933). */
+int32_t statecentric_gdn_state_codec_prepare_decode_pair_bf16_launch_v1(
+    void* stream, const uint16_t* keys, const uint16_t* queries,
+    const float* decay, const float* smoothing, int8_t* quantized,
+    float* dynamic_scale, uint32_t states);
+
+/* Replaces windowed_gdn_kernel.h:139-149 (encoded_projection.cpp:624-776, 935-963). */
+int32_t statecentric_gdn_state_codec_finish_decode_pair_bf16_launch_v1(
+    void* stream, const int32_t* projected, const float* dynamic_scale,
+    const float* scales, const uint16_t* compensator_keys,
+    const uint16_t* compensator_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    const float* decay, const uint16_t* beta, const uint16_t* keys,
+    const uint16_t* queries, const uint16_t* values, uint16_t* outputs,
+    uint32_t states);
+
+/* c[s] = a[s] (transposed when transpose_a) x b[s], a int8 [128][128], b int8
+ * [128][16], c int32 [128][16], exact.  Admission as the reference: workspace
+ * and tiling non-null (they are not read here), 1 <= states <= 128,
+ * blocks == (states + 1) / 2, transpose_a <= 1.  Replaces
+ * windowed_gdn_kernel.h:108-111 (kernel/gdn_state_codec_int8_cube_matmul.cpp:53-68). */
+int32_t statecentric_gdn_state_codec_int8_cube_matmul_launch_v1(
+    void* stream, const int8_t* a, const int8_t* b, int32_t* c, uint32_t states,
+    uint32_t transpose_a, void* workspace, void* tiling, uint32_t blocks);
+
+/* ---- decode runtime (host/gdn_state_codec_decode_runtime.cpp:72-148) ------
+ * create returns a process-wide handle for `states` (1..16384; nullptr when a
+ * live handle has a different count), reference-counted; destroy drops one
+ * reference and ignores foreign handles.  step runs prepare_decode_pair_bf16,
+ * the int8 projection and finish_decode_pair_bf16 as ONE fused kernel (one
+ * pass over the codes), with results bit-identical to running the three
+ * stages; it returns 1 for a bad handle/stream/count.  Unlike the reference,
+ * whose Cube GEMM admits at most 128 states, every admitted count runs. */
+void* statecentric_gdn_state_codec_decode_runtime_create_v1(uint32_t states);
+void statecentric_gdn_state_codec_decode_runtime_destroy_v1(void* runtime);
+int32_t statecentric_gdn_state_codec_decode_runtime_step_v1(
+    void* runtime, void* stream, const int8_t* residual, const float* smoothing,
+    const float* scales, const uint16_t* compensator_keys,
+    const uint16_t* compensator_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    const float* decay, const uint16_t* beta, const uint16_t* keys,
+    const uint16_t* queries, const uint16_t* values, uint16_t* outputs,
+    uint32_t states);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_STATE_CODEC_WINDOW_H */

@@ -87,3 +87,65 @@ def test_null_and_out_of_range_arguments_return_status_1(lib):
     assert lib.encoded_projection_decode_launch_v4(None, p, p, p, p, p, 0, 32, 16, 1.0, 1) == 1
     assert lib.encoded_projection_chunked_launch_v4(None, p, p, p, p, p, 1, 0, 32, 16, 1.0, 1) == 1
     assert lib.encoded_projection_chunked_launch_v4(None, p, p, p, p, p, 1, 4, 32, 16, 1.0, 7) == 1
+
+
+def test_windowed_entry_points_admit_like_the_reference(lib):
+    """windowed_gdn_step.cpp:675-678, 729-734, 757-762; encoded_projection.cpp:
+    867-963; int8_cube_matmul.cpp:57-63: status 1 for a null pointer, a count
+    outside 1..16384 and (bf16) an odd count, before any device work."""
+    p = ctypes.c_void_p(16)
+    sixteen = [p] * 15
+    for states in (0, 16385):
+        assert lib.windowed_gdn_step_launch_v1(None, *sixteen, states) == 1
+        assert lib.windowed_gdn_step_bf16_launch_v1(None, *sixteen, states) == 1
+        assert lib.windowed_gdn_step_bf16_quant_only_launch_v1(None, *sixteen, states) == 1
+        assert lib.fp32_gdn_step_launch_v1(None, *([p] * 7), states) == 1
+        assert lib.prepare_int8_vector_launch_v1(None, p, p, p, p, states) == 1
+        assert lib.prepare_decode_pair_launch_v1(None, *([p] * 6), states) == 1
+        assert lib.prepare_decode_pair_bf16_launch_v1(None, *([p] * 6), states) == 1
+        assert lib.finish_decode_pair_launch_v1(None, *sixteen, states) == 1
+        assert lib.finish_decode_pair_bf16_launch_v1(None, *sixteen, states) == 1
+    assert lib.windowed_gdn_step_bf16_launch_v1(None, *sixteen, 7) == 1
+    assert lib.windowed_gdn_step_bf16_quant_only_launch_v1(None, *sixteen, 7) == 1
+    assert lib.prepare_decode_pair_bf16_launch_v1(None, *([p] * 6), 7) == 1
+    assert lib.finish_decode_pair_bf16_launch_v1(None, *sixteen, 7) == 1
+    for i in range(15):  # every pointer is required, compensators included
+        args = list(sixteen)
+        args[i] = None
+        assert lib.windowed_gdn_step_bf16_quant_only_launch_v1(None, *args, 2) == 1
+        assert lib.windowed_gdn_step_launch_v1(None, *args, 2) == 1
+    # int8 projection: states 1..128, blocks == (states + 1) / 2, workspace and
+    # tiling present, transpose_a <= 1.
+    assert lib.int8_cube_matmul_launch_v1(None, p, p, p, 129, 0, p, p, 65) == 1
+    assert lib.int8_cube_matmul_launch_v1(None, p, p, p, 8, 0, p, p, 3) == 1
+    assert lib.int8_cube_matmul_launch_v1(None, p, p, p, 8, 2, p, p, 4) == 1
+    assert lib.int8_cube_matmul_launch_v1(None, p, p, p, 8, 0, None, p, 4) == 1
+
+
+def test_decode_runtime_lifecycle(lib):
+    """decode_runtime.cpp:72-148: one live handle per process, bound to its
+    state count, reference-counted; foreign handles are rejected."""
+    p = ctypes.c_void_p(16)
+    assert not lib.decode_runtime_create_v1(0)
+    assert not lib.decode_runtime_create_v1(16385)
+    a = lib.decode_runtime_create_v1(64)
+    assert a
+    assert lib.decode_runtime_create_v1(64) == a
+    assert not lib.decode_runtime_create_v1(32)
+    assert lib.decode_runtime_step_v1(a, None, *([p] * 15), 32) == 1  # other count
+    assert lib.decode_runtime_step_v1(p, None, *([p] * 15), 64) == 1  # foreign handle
+    assert lib.decode_runtime_step_v1(a, None, *([p] * 15), 63) == 1
+    args = [p] * 15
+    args[11] = None  # keys: the prepare stage's argument
+    assert lib.decode_runtime_step_v1(a, None, *args, 64) == 2
+    args = [p] * 15
+    args[14] = None  # outputs: the finish stage's argument
+    assert lib.decode_runtime_step_v1(a, None, *args, 64) == 4
+    lib.decode_runtime_destroy_v1(p)  # ignored
+    lib.decode_runtime_destroy_v1(a)
+    assert lib.decode_runtime_create_v1(64) == a  # still live: one reference left
+    lib.decode_runtime_destroy_v1(a)
+    lib.decode_runtime_destroy_v1(a)
+    b = lib.decode_runtime_create_v1(32)  # released: a new count is accepted
+    assert b
+    lib.decode_runtime_destroy_v1(b)
