@@ -222,6 +222,98 @@ def bench_chunked_projection(steps: int, warmup: int):
     return us
 
 
+WINDOW_STATES = 256 * 32  # B = 256 sequences x 32 value heads
+
+
+def window_step_bytes(position: int, compensated: bool) -> int:
+    """Algorithmic HBM bytes of one windowed bf16 step on one state at window
+    position p: the int8 boundary with its smoothing and scales, the model
+    vectors (a key/query pair is shared by two value heads), p stored records
+    read, the new record, output and position written."""
+    boundary = 128 * 128 + 2 * 128 * 4
+    vectors = (2 * 128 * 2) // 2 + 128 * 2 + 4 + 2     # k,q / 2, values, log decay, beta
+    compensators = 2 * 128 * 4 * 2 if compensated else 0
+    records = position * (2 * 128 * 2 + 4)             # keys + corrections + gate
+    writes = 128 * 2 + 2 * 128 * 2 + 4                 # output, record key + correction, gate
+    return boundary + vectors + compensators + records + writes + 4 + 4  # position in/out
+
+
+def bench_window_step(warmup: int):
+    """The windowed decode step at B=256 (8192 states): 5 slot copies, each
+    stepped through a whole window (positions 0..15) between one event pair,
+    launches interleaved across copies so consecutive launches touch different
+    states."""
+    import torch
+
+    from gdn_state_codec import codec
+    from gdn_state_codec.window import DecodeRuntime, WindowSlot, step_bf16
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    states = WINDOW_STATES
+    slots, inputs = [], []
+    for _ in range(ROTATIONS):
+        x = _c1_style_state((states, 128, 128), gen, dev)
+        slot = WindowSlot.allocate(states, dev)
+        codec.encode(x, codec.LAYOUT_VALUE_KEY, slot.residual, slot.smoothing, slot.scales)
+        slot.compensator_keys.copy_(torch.randn(slot.compensator_keys.shape, generator=gen,
+                                                device=dev) * 0.01)
+        slot.compensator_values.copy_(torch.randn(slot.compensator_values.shape, generator=gen,
+                                                  device=dev) * 0.01)
+        del x
+        k = torch.randn((states // 2, 128), generator=gen, device=dev)
+        q = torch.randn((states // 2, 128), generator=gen, device=dev)
+        inputs.append(dict(
+            log_decay=torch.log(0.9 + 0.09 * torch.rand(states, generator=gen, device=dev)),
+            beta=(0.2 + 0.6 * torch.rand(states, generator=gen, device=dev)).to(torch.bfloat16),
+            keys=(k / k.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
+            queries=(q / q.norm(dim=-1, keepdim=True)).to(torch.bfloat16),
+            values=(0.5 * torch.randn((states, 128), generator=gen, device=dev)).to(torch.bfloat16)))
+        slots.append(slot)
+    outs = [torch.empty((states, 128), dtype=torch.bfloat16, device=dev) for _ in range(ROTATIONS)]
+    runtime = DecodeRuntime(states)
+    kinds = {
+        "quant_only": lambda r: step_bf16(slots[r], **inputs[r], out=outs[r], quant_only=True,
+                                          validate=False),
+        "compensated": lambda r: step_bf16(slots[r], **inputs[r], out=outs[r], validate=False),
+        "decode_runtime": lambda r: runtime.step(slots[r], **inputs[r], out=outs[r],
+                                                 validate=False),
+    }
+    results = {}
+    for name, run in kinds.items():
+        for _ in range(max(warmup, 1)):
+            for slot in slots:
+                slot.positions.zero_()
+            for t in range(16):
+                for r in range(ROTATIONS):
+                    run(r)
+        for slot in slots:
+            slot.positions.zero_()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for t in range(16):
+            for r in range(ROTATIONS):
+                run(r)
+        b.record()
+        launches = 16 * ROTATIONS
+        us = _events_ms([(a, b)])[0] / launches * 1e3
+        assert all(bool((slot.positions[:, 0] == 16).all()) for slot in slots)
+        compensated = name != "quant_only"
+        nbytes = sum(window_step_bytes(p, compensated) for p in range(16)) * states / 16
+        results[name] = {"us_per_step": us, "GBps": nbytes / (us * 1e-6) / 1e9,
+                         "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+                         "bytes_per_step": nbytes}
+        _log(f"windowed step {name}: {us:.2f} us/step, {results[name]['GBps']:.0f} GB/s")
+    runtime.close()
+    results["workload"] = ("windowed bf16 decode step, B=256 x 32 value heads (GQA from 16), "
+                           "int8 [value][key] boundary, positions 0..15 averaged")
+    results["rotated_state_copies"] = ROTATIONS
+    del slots, inputs, outs
+    return results
+
+
 def bench_pool(steps: int, warmup: int):
     """Config 5 with a bf16 pool (64.4 GB): gather-encode and decode-scatter."""
     import torch
@@ -331,6 +423,7 @@ def profile_pass() -> int:
     bench_hbm_probe(repeats=2)
     bench_decode_projection(1, 0)
     bench_chunked_projection(1, 0)
+    bench_window_step(0)
     torch.cuda.synchronize()
     print(json.dumps({"profile_pass": "done"}), flush=True)
     return 0
@@ -387,6 +480,8 @@ def main() -> int:
             "TFLOPs": C4_FLOPS / (chunk_us * 1e-6) / 1e12,
             "mfma_frac_of_useful_flops": C4_FLOPS / (chunk_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
             "bytes_per_step": C4_BYTES, "rotated_state_copies": ROTATIONS}
+        torch.cuda.empty_cache()
+        extra["windowed_step"] = bench_window_step(args.warmup)
     if args.pool:
         extra["pool_codec"] = bench_pool(max(args.steps // 4, 2), 1)
     line = {

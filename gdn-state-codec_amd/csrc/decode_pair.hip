@@ -185,11 +185,13 @@ struct FinishArgs {
   bool bf16;
 };
 
-// LDS a wavefront needs for the finish: the three vectors and the 41 sums.
+// LDS a wavefront needs for the finish: the three vectors, the compensator
+// and record keys widened to fp32 (rows 0..3 and 4..4+p-1), and the 41 sums.
 struct FinishShared {
   float read[kDim];
   float query[kDim];
   float write[kDim];
+  float basis[kRank + kWindow][kDim];
   float sums[1 + 2 * kRank + 2 * kWindow];
 };
 
@@ -208,32 +210,57 @@ __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& 
     sh.query[2 * lane + e] = v.query[e];
     sh.write[2 * lane + e] = v.write[e];
   }
+  {
+    // comp_keys [state][key][4]: this lane's two keys are 8 contiguous halves.
+    const uint4 ck = *reinterpret_cast<const uint4*>(a.comp_keys + (vector_base + 2 * lane) * kRank);
+    const uint32_t words[4] = {ck.x, ck.y, ck.z, ck.w};
+#pragma unroll
+    for (int r = 0; r < kRank; ++r) {
+      sh.basis[r][2 * lane] = half_bits_to_float((words[r >> 1] >> (16 * (r & 1))) & 0xFFFFu);
+      sh.basis[r][2 * lane + 1] =
+          half_bits_to_float((words[2 + (r >> 1)] >> (16 * (r & 1))) & 0xFFFFu);
+    }
+#pragma unroll
+    for (int j = 0; j < kWindow; ++j) {
+      if (j < static_cast<int>(p)) {
+        const uint32_t rk = *reinterpret_cast<const uint32_t*>(
+            a.record_keys + (record_base + j) * kDim + 2 * lane);
+        sh.basis[kRank + j][2 * lane] = half_bits_to_float(rk & 0xFFFFu);
+        sh.basis[kRank + j][2 * lane + 1] = half_bits_to_float(rk >> 16);
+      }
+    }
+  }
   wave_lds_sync();
   // Sequential sums in row order, one per lane: 0 = update, 1..4 = old read
   // projections, 5..8 = old output projections, 9.. = record read projections
-  // then record output projections.
+  // then record output projections.  Each is the reference's
+  // acc += basis * x (read side) or acc += basis * query * gate (output side).
   const int sums = 1 + 2 * kRank + 2 * static_cast<int>(p);
   if (lane < sums) {
-    float acc = 0.0f;
+    const float* basis;
+    const float* x;
+    bool gated;
     if (lane == 0) {
-      for (int row = 0; row < kDim; ++row) acc += sh.write[row] * sh.query[row];
+      basis = sh.write;
+      x = sh.query;
+      gated = false;
     } else if (lane <= 2 * kRank) {
-      const int r = (lane - 1) & (kRank - 1);
-      const bool out_side = lane > kRank;
-      const uint16_t* basis = a.comp_keys + vector_base * kRank + r;
-      for (int row = 0; row < kDim; ++row) {
-        const float b = half_bits_to_float(basis[row * kRank]);
-        acc += out_side ? b * sh.query[row] * v.gate : b * sh.read[row];
-      }
+      basis = sh.basis[(lane - 1) & (kRank - 1)];
+      gated = lane > kRank;
+      x = gated ? sh.query : sh.read;
     } else {
       const int index = lane - 1 - 2 * kRank;
-      const bool out_side = index >= static_cast<int>(p);
-      const int j = out_side ? index - static_cast<int>(p) : index;
-      const uint16_t* basis = a.record_keys + (record_base + j) * kDim;
-      for (int row = 0; row < kDim; ++row) {
-        const float b = half_bits_to_float(basis[row]);
-        acc += out_side ? b * sh.query[row] * v.gate : b * sh.read[row];
-      }
+      gated = index >= static_cast<int>(p);
+      basis = sh.basis[kRank + (gated ? index - static_cast<int>(p) : index)];
+      x = gated ? sh.query : sh.read;
+    }
+    float acc = 0.0f;
+    if (gated) {
+#pragma unroll 16
+      for (int row = 0; row < kDim; ++row) acc += basis[row] * x[row] * v.gate;
+    } else {
+#pragma unroll 16
+      for (int row = 0; row < kDim; ++row) acc += basis[row] * x[row];
     }
     sh.sums[lane] = acc;
   }
@@ -471,6 +498,17 @@ __global__ __launch_bounds__(kThreads) void fused_decode_pair_kernel(
   const uint32_t p = fa.positions[static_cast<uint64_t>(state) * kPositionStride];
   if (p >= kWindow) return;
 
+  // The codes first (the bulk of the traffic), in flight during the prepare.
+  // Lane owns keys 16*kq..+15 of value rows r8 + 8j.
+  const int kq = lane & 7;
+  const int r8 = lane >> 3;
+  const int8_t* codes = residual + static_cast<uint64_t>(state) * kTile;
+  uint4 row[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    row[j] = stream_load(reinterpret_cast<const uint4*>(codes + (r8 + 8 * j) * kDim + 16 * kq));
+  }
+
   const StepVectors v = load_vectors(in, state, lane);
   float pair[2][2];
   prepare_pairs(v, in.bf16, smoothing, state, lane, pair);
@@ -492,15 +530,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_pair_kernel(
   }
   wave_lds_sync();
 
-  // Projection: lane owns keys 16*kq..+15 of value rows r8 + 8j.
-  const int kq = lane & 7;
-  const int r8 = lane >> 3;
-  const int8_t* codes = residual + static_cast<uint64_t>(state) * kTile;
-  uint4 row[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    row[j] = stream_load(reinterpret_cast<const uint4*>(codes + (r8 + 8 * j) * kDim + 16 * kq));
-  }
+  // Projection of the codes against the four quantized vectors.
   int qv[4][4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {

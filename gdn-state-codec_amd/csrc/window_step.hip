@@ -97,12 +97,42 @@ __device__ __forceinline__ void reduce16_over_8_lanes(float (&p)[16], int lane,
   }
 }
 
+// Reduce-scatter of N partial sums over the 64 lanes: log2(N) halving steps
+// over lane bits 5, 4, ... followed by a plain sum over the remaining low bits
+// leave lane L holding the total of value L >> (6 - log2(N)).
+template <int N, int kMask>
+__device__ __forceinline__ void halve(float* v, int lane) {
+  if constexpr (N > 1) {
+    constexpr int n = N / 2;
+    const bool up = (lane & kMask) != 0;
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+      const float send = up ? v[i] : v[i + n];
+      const float keep = up ? v[i + n] : v[i];
+      v[i] = keep + __shfl_xor(send, kMask);
+    }
+    halve<n, kMask / 2>(v, lane);
+  }
+}
+
+template <int N>
+__device__ __forceinline__ float reduce_scatter(float (&v)[N], int lane) {
+  halve<N, 32>(v, lane);
+  float x = v[0];
+#pragma unroll
+  for (int mask = 32 / N; mask >= 1; mask >>= 1) x += __shfl_xor(x, mask);
+  return x;
+}
+
 template <int kVariant>
 __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
   constexpr bool kValueKey = kVariant != kStepF16;
   constexpr bool kCompensated = kVariant != kStepBF16QuantOnly;
   __shared__ __align__(16) float weights[kWaves][2][kDim];  // s*read, s*output vector
-  __shared__ float coefficients[kWaves][2][kWindow];
+  __shared__ __align__(16) float readouts[kWaves][2][kDim]; // boundary readouts by value
+  // [0, 16): record read-side coefficients, [16, 32): output side,
+  // [32, 36) / [36, 40): compensator read / output projections.
+  __shared__ float coefficients[kWaves][2 * kWindow + 2 * kRank];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -113,48 +143,73 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
 
   const uint64_t vector_base = static_cast<uint64_t>(state) * kDim;
   const uint64_t record_base = static_cast<uint64_t>(state) * kWindow;
+  const int k0 = 2 * lane;  // this lane's two keys, and (phase 3) its two values
 
-  // ---- phase 1: vectors, update, compensator and record projections --------
-  const int k0 = 2 * lane;
-  float g, read0, read1, out0, out1, write0, write1, query0, query1;
-  uint32_t record_key_bits;
+  // ---- loads, in the order they are consumed: memory returns in issue order,
+  // so phase 1 waits only for its own operands while the 16 KiB of codes is
+  // still in flight.
+  uint32_t vec_a, vec_b, vec_c = 0;
+  float g, beta = 0.0f;
   if constexpr (kVariant == kStepF16) {
     g = a.decay[state];
-    const uint32_t wk = *reinterpret_cast<const uint32_t*>(a.keys + vector_base + k0);
-    const uint32_t rd = *reinterpret_cast<const uint32_t*>(a.reads + vector_base + k0);
-    const uint32_t qr = *reinterpret_cast<const uint32_t*>(a.queries + vector_base + k0);
-    write0 = half_bits_to_float(wk & 0xFFFFu);
-    write1 = half_bits_to_float(wk >> 16);
-    read0 = half_bits_to_float(rd & 0xFFFFu);
-    read1 = half_bits_to_float(rd >> 16);
-    query0 = half_bits_to_float(qr & 0xFFFFu);
-    query1 = half_bits_to_float(qr >> 16);
-    out0 = query0 * g;
-    out1 = query1 * g;
-    record_key_bits = wk;
+    vec_a = *reinterpret_cast<const uint32_t*>(a.keys + vector_base + k0);     // write keys
+    vec_b = *reinterpret_cast<const uint32_t*>(a.queries + vector_base + k0);
+    vec_c = *reinterpret_cast<const uint32_t*>(a.reads + vector_base + k0);
   } else {
     g = decay_gate(a.decay[state]);
-    const float beta = bf16_to_float(a.beta[state]);
+    beta = bf16_to_float(a.beta[state]);
     const uint64_t head = static_cast<uint64_t>(state >> 1) * kDim + k0;
-    const uint32_t kw = *reinterpret_cast<const uint32_t*>(a.keys + head);
-    const uint32_t qw = *reinterpret_cast<const uint32_t*>(a.queries + head);
-    const float key0 = bf16_to_float(kw & 0xFFFFu);
-    const float key1 = bf16_to_float(kw >> 16);
-    query0 = kQueryScale * bf16_to_float(qw & 0xFFFFu);
-    query1 = kQueryScale * bf16_to_float(qw >> 16);
+    vec_a = *reinterpret_cast<const uint32_t*>(a.keys + head);
+    vec_b = *reinterpret_cast<const uint32_t*>(a.queries + head);
+  }
+  const float2 sm = *reinterpret_cast<const float2*>(a.smoothing + vector_base + k0);
+  uint32_t record_key[kWindow];
+#pragma unroll
+  for (int j = 0; j < kWindow; ++j) {
+    record_key[j] = j < static_cast<int>(p)
+        ? *reinterpret_cast<const uint32_t*>(a.record_keys + (record_base + j) * kDim + k0)
+        : 0u;
+  }
+  uint4 comp_key = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (kCompensated) {
+    comp_key = *reinterpret_cast<const uint4*>(a.comp_keys + (vector_base + k0) * kRank);
+  }
+  // Lane (c, r) = (lane & 7, lane >> 3) reads bytes 16c..16c+15 of rows r + 8j.
+  const int8_t* codes = a.residual + static_cast<uint64_t>(state) * kTile;
+  const int chunk = lane & 7;
+  const int row8 = lane >> 3;
+  uint4 row[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    row[j] = stream_load(reinterpret_cast<const uint4*>(codes + (row8 + 8 * j) * kDim + 16 * chunk));
+  }
+
+  // ---- phase 1: vectors, update, compensator and record projections --------
+  float read0, read1, out0, out1, write0, write1, query0, query1;
+  uint32_t record_key_bits;
+  if constexpr (kVariant == kStepF16) {
+    write0 = half_bits_to_float(vec_a & 0xFFFFu);
+    write1 = half_bits_to_float(vec_a >> 16);
+    query0 = half_bits_to_float(vec_b & 0xFFFFu);
+    query1 = half_bits_to_float(vec_b >> 16);
+    read0 = half_bits_to_float(vec_c & 0xFFFFu);
+    read1 = half_bits_to_float(vec_c >> 16);
+    record_key_bits = vec_a;
+  } else {
+    const float key0 = bf16_to_float(vec_a & 0xFFFFu);
+    const float key1 = bf16_to_float(vec_a >> 16);
+    query0 = kQueryScale * bf16_to_float(vec_b & 0xFFFFu);
+    query1 = kQueryScale * bf16_to_float(vec_b >> 16);
     read0 = g * key0;
     read1 = g * key1;
-    out0 = query0 * g;
-    out1 = query1 * g;
     write0 = beta * key0;
     write1 = beta * key1;
     record_key_bits = float_to_half_bits(write0) | (float_to_half_bits(write1) << 16);
   }
-  {
-    const float2 sm = *reinterpret_cast<const float2*>(a.smoothing + vector_base + k0);
-    *reinterpret_cast<float2*>(&weights[wave][0][k0]) = make_float2(sm.x * read0, sm.y * read1);
-    *reinterpret_cast<float2*>(&weights[wave][1][k0]) = make_float2(sm.x * out0, sm.y * out1);
-  }
+  out0 = query0 * g;
+  out1 = query1 * g;
+  *reinterpret_cast<float2*>(&weights[wave][0][k0]) = make_float2(sm.x * read0, sm.y * read1);
+  *reinterpret_cast<float2*>(&weights[wave][1][k0]) = make_float2(sm.x * out0, sm.y * out1);
   const float update = wave_sum(write0 * query0 + write1 * query1);
 
   // Gate products: suffix_j = prod_{i > j} gate_i over the p stored records.
@@ -166,54 +221,64 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
     if (j < static_cast<int>(p)) boundary_suffix *= a.record_decay[record_base + j];
   }
 
-  float comp_read[kRank], comp_out[kRank];
+  // Record projections key_j . read and key_j . (q*g): 32 partials, one
+  // reduce-scatter; lane L ends with value L >> 1.
+  {
+    float partial[2 * kWindow];
+#pragma unroll
+    for (int j = 0; j < kWindow; ++j) {
+      const float b0 = half_bits_to_float(record_key[j] & 0xFFFFu);
+      const float b1 = half_bits_to_float(record_key[j] >> 16);
+      partial[j] = b0 * read0 + b1 * read1;
+      partial[kWindow + j] = b0 * out0 + b1 * out1;
+    }
+    const float total = reduce_scatter(partial, lane);
+    const int index = lane >> 1;
+    const int j = index & (kWindow - 1);
+    float sfx = 1.0f;
+#pragma unroll
+    for (int jj = 0; jj < kWindow; ++jj) sfx = jj == j ? suffix[jj] : sfx;
+    if ((lane & 1) == 0) coefficients[wave][index] = total * sfx;
+  }
   if constexpr (kCompensated) {
-    // comp_keys [state][key][4]: this lane's two keys are 8 contiguous halves.
-    const uint4 ck = *reinterpret_cast<const uint4*>(a.comp_keys + (vector_base + k0) * kRank);
-    const uint32_t words[4] = {ck.x, ck.y, ck.z, ck.w};
+    const uint32_t words[4] = {comp_key.x, comp_key.y, comp_key.z, comp_key.w};
+    float partial[2 * kRank];
 #pragma unroll
     for (int r = 0; r < kRank; ++r) {
       const float b0 = half_bits_to_float((words[r >> 1] >> (16 * (r & 1))) & 0xFFFFu);
       const float b1 = half_bits_to_float((words[2 + (r >> 1)] >> (16 * (r & 1))) & 0xFFFFu);
-      comp_read[r] = wave_sum(b0 * read0 + b1 * read1) * boundary_suffix;
-      comp_out[r] = wave_sum(b0 * out0 + b1 * out1) * boundary_suffix;
+      partial[r] = b0 * read0 + b1 * read1;
+      partial[kRank + r] = b0 * out0 + b1 * out1;
     }
+    const float total = reduce_scatter(partial, lane);  // lane L: value L >> 3
+    if ((lane & 7) == 0) coefficients[wave][2 * kWindow + (lane >> 3)] = total * boundary_suffix;
   }
+
+  // Phase-3 operands for values k0, k0+1, in flight during phase 2.
+  uint32_t correction_word[kWindow];
 #pragma unroll
   for (int j = 0; j < kWindow; ++j) {
-    if (j < static_cast<int>(p)) {
-      const uint32_t rk = *reinterpret_cast<const uint32_t*>(
-          a.record_keys + (record_base + j) * kDim + k0);
-      const float b0 = half_bits_to_float(rk & 0xFFFFu);
-      const float b1 = half_bits_to_float(rk >> 16);
-      const float pr = wave_sum(b0 * read0 + b1 * read1) * suffix[j];
-      const float po = wave_sum(b0 * out0 + b1 * out1) * suffix[j];
-      if (lane == 0) {
-        coefficients[wave][0][j] = pr;
-        coefficients[wave][1][j] = po;
-      }
-    }
+    correction_word[j] = j < static_cast<int>(p)
+        ? *reinterpret_cast<const uint32_t*>(a.record_corrections + (record_base + j) * kDim + k0)
+        : 0u;
+  }
+  const float2 scale = *reinterpret_cast<const float2*>(a.scales + vector_base + k0);
+  const uint32_t value_word = *reinterpret_cast<const uint32_t*>(a.values + vector_base + k0);
+  uint4 comp_value = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (kCompensated) {
+    comp_value = *reinterpret_cast<const uint4*>(a.comp_values + (vector_base + k0) * kRank);
   }
   wave_lds_sync();
 
-  // ---- phase 2: both boundary readouts from one pass over the codes --------
+  // ---- phase 2: both boundary readouts from the codes in registers ---------
   float acc_read[16], acc_out[16];
-  int value_of[2];
-  const int8_t* codes = a.residual + static_cast<uint64_t>(state) * kTile;
   if constexpr (kValueKey) {
-    // codes [value][key]: lane owns keys 16*kq..+15 of value rows r8 + 8j.
-    const int kq = lane & 7;
-    const int r8 = lane >> 3;
-    uint4 row[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      row[j] = stream_load(reinterpret_cast<const uint4*>(codes + (r8 + 8 * j) * kDim + 16 * kq));
-    }
+    // codes [value][key]: lane owns keys 16*chunk..+15 of value rows row8 + 8j.
     float wr[16], wo[16];
 #pragma unroll
     for (int i = 0; i < 16; i += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(&weights[wave][0][16 * kq + i]);
-      const float4 y = *reinterpret_cast<const float4*>(&weights[wave][1][16 * kq + i]);
+      const float4 x = *reinterpret_cast<const float4*>(&weights[wave][0][16 * chunk + i]);
+      const float4 y = *reinterpret_cast<const float4*>(&weights[wave][1][16 * chunk + i]);
       wr[i] = x.x; wr[i + 1] = x.y; wr[i + 2] = x.z; wr[i + 3] = x.w;
       wo[i] = y.x; wo[i + 1] = y.y; wo[i + 2] = y.z; wo[i + 3] = y.w;
     }
@@ -231,17 +296,14 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
     }
     reduce16_over_8_lanes(acc_read, lane, 4, 2, 1);
     reduce16_over_8_lanes(acc_out, lane, 4, 2, 1);
-    value_of[0] = r8 + 8 * (2 * kq);
-    value_of[1] = r8 + 8 * (2 * kq + 1);
-  } else {
-    // codes [key][value]: lane owns values 16*vc..+15 of key rows kr + 8j.
-    const int vc = lane & 7;
-    const int kr = lane >> 3;
-    uint4 row[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      row[j] = stream_load(reinterpret_cast<const uint4*>(codes + (kr + 8 * j) * kDim + 16 * vc));
+    for (int e = 0; e < 2; ++e) {
+      const int v = row8 + 8 * (2 * chunk + e);
+      readouts[wave][0][v] = acc_read[e];
+      readouts[wave][1][v] = acc_out[e];
     }
+  } else {
+    // codes [key][value]: lane owns values 16*chunk..+15 of key rows row8 + 8j.
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       acc_read[i] = 0.0f;
@@ -249,8 +311,8 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const float wr = weights[wave][0][kr + 8 * j];
-      const float wo = weights[wave][1][kr + 8 * j];
+      const float wr = weights[wave][0][row8 + 8 * j];
+      const float wo = weights[wave][1][row8 + 8 * j];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float c = code_byte(word_of(row[j], i >> 2), i & 3);
@@ -260,50 +322,65 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
     }
     reduce16_over_8_lanes(acc_read, lane, 32, 16, 8);
     reduce16_over_8_lanes(acc_out, lane, 32, 16, 8);
-    value_of[0] = 16 * vc + 2 * kr;
-    value_of[1] = 16 * vc + 2 * kr + 1;
+    // values 16*chunk + 2*row8 + {0, 1}: adjacent, one 8-byte LDS store each.
+    const int v = 16 * chunk + 2 * row8;
+    *reinterpret_cast<float2*>(&readouts[wave][0][v]) = make_float2(acc_read[0], acc_read[1]);
+    *reinterpret_cast<float2*>(&readouts[wave][1][v]) = make_float2(acc_out[0], acc_out[1]);
   }
+  wave_lds_sync();
 
-  // ---- phase 3: finish two values per lane ----------------------------------
-  uint16_t* correction_out = a.record_corrections + (record_base + p) * kDim;
+  // ---- phase 3: finish values k0, k0+1 --------------------------------------
+  const float2 sr = *reinterpret_cast<const float2*>(&readouts[wave][0][k0]);
+  const float2 so = *reinterpret_cast<const float2*>(&readouts[wave][1][k0]);
+  const float boundary_read[2] = {sr.x, sr.y};
+  const float boundary_out[2] = {so.x, so.y};
+  const float value_scale[2] = {scale.x, scale.y};
+  const uint32_t comp_words[4] = {comp_value.x, comp_value.y, comp_value.z, comp_value.w};
+  uint32_t output_bits = 0, correction_bits = 0;
+  float output_f32[2];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const int v = value_of[e];
-    const float factor = a.scales[vector_base + v] * boundary_suffix * kInvQuantizedMaximum;
-    float state_read = acc_read[e] * factor;
-    float output_read = acc_out[e] * factor;
+    const float factor = value_scale[e] * boundary_suffix * kInvQuantizedMaximum;
+    float state_read = boundary_read[e] * factor;
+    float output_read = boundary_out[e] * factor;
     if constexpr (kCompensated) {
-      const uint2 cv = *reinterpret_cast<const uint2*>(a.comp_values + (vector_base + v) * kRank);
 #pragma unroll
       for (int r = 0; r < kRank; ++r) {
-        const float b = half_bits_to_float(((r < 2 ? cv.x : cv.y) >> (16 * (r & 1))) & 0xFFFFu);
-        state_read = fmaf(b, comp_read[r], state_read);
-        output_read = fmaf(b, comp_out[r], output_read);
+        const float b = half_bits_to_float(
+            (comp_words[2 * e + (r >> 1)] >> (16 * (r & 1))) & 0xFFFFu);
+        state_read = fmaf(b, coefficients[wave][2 * kWindow + r], state_read);
+        output_read = fmaf(b, coefficients[wave][2 * kWindow + kRank + r], output_read);
       }
     }
 #pragma unroll
     for (int j = 0; j < kWindow; ++j) {
       if (j < static_cast<int>(p)) {
-        const float c = half_bits_to_float(a.record_corrections[(record_base + j) * kDim + v]);
-        state_read = fmaf(c, coefficients[wave][0][j], state_read);
-        output_read = fmaf(c, coefficients[wave][1][j], output_read);
+        const float c = half_bits_to_float((correction_word[j] >> (16 * e)) & 0xFFFFu);
+        state_read = fmaf(c, coefficients[wave][j], state_read);
+        output_read = fmaf(c, coefficients[wave][kWindow + j], output_read);
       }
     }
     float value;
     if constexpr (kVariant == kStepF16) {
-      value = half_bits_to_float(a.values[vector_base + v]);
+      value = half_bits_to_float((value_word >> (16 * e)) & 0xFFFFu);
     } else {
-      value = bf16_to_float(a.values[vector_base + v]);
+      value = bf16_to_float((value_word >> (16 * e)) & 0xFFFFu);
     }
     const float correction = value - state_read;
     const float out = fmaf(correction, update, output_read);
-    if constexpr (kVariant == kStepF16) {
-      static_cast<float*>(a.outputs)[vector_base + v] = out;
-    } else {
-      static_cast<uint16_t*>(a.outputs)[vector_base + v] = float_to_bf16(out);
-    }
-    correction_out[v] = static_cast<uint16_t>(float_to_half_bits(correction));
+    output_f32[e] = out;
+    output_bits |= static_cast<uint32_t>(float_to_bf16(out)) << (16 * e);
+    correction_bits |= float_to_half_bits(correction) << (16 * e);
   }
+  if constexpr (kVariant == kStepF16) {
+    *reinterpret_cast<float2*>(static_cast<float*>(a.outputs) + vector_base + k0) =
+        make_float2(output_f32[0], output_f32[1]);
+  } else {
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.outputs) + vector_base + k0) =
+        output_bits;
+  }
+  *reinterpret_cast<uint32_t*>(a.record_corrections + (record_base + p) * kDim + k0) =
+      correction_bits;
   *reinterpret_cast<uint32_t*>(a.record_keys + (record_base + p) * kDim + k0) = record_key_bits;
   if (lane == 0) {
     a.record_decay[record_base + p] = g;
