@@ -1,0 +1,316 @@
+// Rank-4 window-boundary refit (window_boundary_launch_v1 with
+// power_iterations in 1..32; native/ascendc/gdn_state_codec/kernel/
+// gdn_state_codec_window_boundary.cpp:253-366).
+//
+// For a state whose 16-record window is full, the window's residual operator
+//   R = boundary * S + old compensators * S + sum_j key_j corr_j^T * suffix_j
+// is fitted with four rank-one terms by deflated power iteration (the start
+// vector of rank r is ((r+1)(c+3)) mod 17 - 8, normalized with a 20-step
+// Newton square root), stored as fp16 compensators; R minus the fit is then
+// re-encoded with fresh smoothing sqrt(mean |row|), absmax scales and
+// round-half-away codes, and the window is cleared.
+//
+// Every dot product of the reference is a sequential fp32 sum; this kernel
+// keeps each one on a single thread in the reference's order (outputs of the
+// operator in parallel, one row or column per thread; projections and norms
+// on single threads, broadcast through LDS), so the result is bit-identical to
+// the CPU statement of the reference kernel.  One 128-thread workgroup per
+// state, operands staged in LDS; the codes use a 132-byte row stride so both
+// the row walk and the column walk are free of bank conflicts.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "codec_math.h"
+#include "gdn_state_codec_window.h"
+#include "launch.h"
+#include "window_common.h"
+
+namespace gdn {
+namespace {
+
+constexpr int kThreads = 128;
+constexpr int kCodeStride = kDim + 4;
+constexpr float kBoundaryFloor = 1.0e-8f;
+
+struct PowerArgs {
+  const int8_t* residual;
+  const float* smoothing;
+  const float* scales;
+  const uint16_t* comp_keys;
+  const uint16_t* comp_values;
+  float* record_decay;
+  uint16_t* record_keys;
+  uint16_t* record_corrections;
+  uint32_t* positions;
+  int8_t* next_residual;
+  float* next_smoothing;
+  float* next_scales;
+  uint16_t* next_comp_keys;
+  uint16_t* next_comp_values;
+  float* workspace;
+  uint32_t power_iterations;
+};
+
+struct PowerShared {
+  int8_t code[kDim * kCodeStride];  // [value column][key row]
+  float ck[kDim * kRank], cv[kDim * kRank];
+  float nk[kDim * kRank], nv[kDim * kRank];
+  float rk[kWindow * kDim], rc[kWindow * kDim];
+  float smoothing[kDim], scales[kDim], next_smoothing[kDim];
+  float left[kDim], right[kDim];
+  float old_projection[kRank], fitted_projection[kRank], record_projection[kWindow];
+  float record_suffix[kWindow];
+  float scalar;  // norm inverse / singular value broadcast
+  int flag;
+};
+
+// window_boundary.cpp:17-23.
+__device__ __forceinline__ float newton_sqrt(float value) {
+  float estimate = value > 1.0f ? value : 1.0f;
+#pragma unroll 1
+  for (int i = 0; i < 20; ++i) estimate = 0.5f * (estimate + value / estimate);
+  return estimate;
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) { return half_bits_to_float(h); }
+__device__ __forceinline__ float round_half(float x) {
+  return half_bits_to_float(float_to_half_bits(x));
+}
+
+// Normalize (:25-37) of v; returns whether the norm was usable.  The squared
+// norm is one sequential sum on thread 0.
+__device__ bool normalize(PowerShared& sh, float* v, int t) {
+  if (t == 0) {
+    float squared = 0.0f;
+    for (int i = 0; i < kDim; ++i) squared += v[i] * v[i];
+    sh.flag = squared <= 1.0e-20f ? 0 : 1;
+    sh.scalar = sh.flag ? 1.0f / newton_sqrt(squared) : 0.0f;
+  }
+  __syncthreads();
+  const bool ok = sh.flag != 0;
+  if (ok) v[t] *= sh.scalar;
+  __syncthreads();
+  return ok;
+}
+
+// Projections of an apply: old compensator side, records, fitted ranks; one
+// sequential sum per thread in the reference's loop order.
+__device__ void projections(PowerShared& sh, const float* vector, const float* old_basis,
+                            const float* record_basis, const float* fitted_basis,
+                            int fitted, int t) {
+  if (t < kRank) {
+    float acc = 0.0f;
+    for (int i = 0; i < kDim; ++i) acc += old_basis[i * kRank + t] * vector[i];
+    sh.old_projection[t] = acc;
+  } else if (t < kRank + kWindow) {
+    const int j = t - kRank;
+    float acc = 0.0f;
+    for (int i = 0; i < kDim; ++i) acc += record_basis[j * kDim + i] * vector[i];
+    sh.record_projection[j] = acc;
+  } else if (t < 2 * kRank + kWindow && t - kRank - kWindow < fitted) {
+    const int r = t - kRank - kWindow;
+    float acc = 0.0f;
+    for (int i = 0; i < kDim; ++i) acc += fitted_basis[i * kRank + r] * vector[i];
+    sh.fitted_projection[r] = acc;
+  }
+  __syncthreads();
+}
+
+// ApplyRight (:113-166): output[row] = R^T-free form R * vector over columns.
+__device__ void apply_right(PowerShared& sh, const float* vector, float* output, float bs,
+                            int fitted, int t) {
+  projections(sh, vector, sh.cv, sh.rc, sh.nv, fitted, t);
+  const int row = t;
+  float value = 0.0f;
+  const float s = sh.smoothing[row];
+  for (int column = 0; column < kDim; ++column) {
+    value += static_cast<float>(sh.code[column * kCodeStride + row]) / 127.0f * s *
+             sh.scales[column] * vector[column] * bs;
+  }
+  for (int r = 0; r < kRank; ++r) value += sh.ck[row * kRank + r] * sh.old_projection[r] * bs;
+  for (int j = 0; j < kWindow; ++j) {
+    value += sh.rk[j * kDim + row] * sh.record_projection[j] * sh.record_suffix[j];
+  }
+  for (int r = 0; r < fitted; ++r) value -= sh.nk[row * kRank + r] * sh.fitted_projection[r];
+  __syncthreads();  // every thread has read `vector` before it may be overwritten
+  output[row] = value;
+  __syncthreads();
+}
+
+// ApplyTranspose (:168-221): output[column] = R^T * vector over rows.
+__device__ void apply_transpose(PowerShared& sh, const float* vector, float* output, float bs,
+                                int fitted, int t) {
+  projections(sh, vector, sh.ck, sh.rk, sh.nk, fitted, t);
+  const int column = t;
+  float value = 0.0f;
+  const float scale = sh.scales[column];
+  const int8_t* code = sh.code + column * kCodeStride;
+  for (int row = 0; row < kDim; ++row) {
+    value += static_cast<float>(code[row]) / 127.0f * sh.smoothing[row] * scale *
+             vector[row] * bs;
+  }
+  for (int r = 0; r < kRank; ++r) value += sh.cv[column * kRank + r] * sh.old_projection[r] * bs;
+  for (int j = 0; j < kWindow; ++j) {
+    value += sh.rc[j * kDim + column] * sh.record_projection[j] * sh.record_suffix[j];
+  }
+  for (int r = 0; r < fitted; ++r) value -= sh.nv[column * kRank + r] * sh.fitted_projection[r];
+  __syncthreads();
+  output[column] = value;
+  __syncthreads();
+}
+
+// ResidualCell (:223-251).
+__device__ __forceinline__ float residual_cell(const PowerShared& sh, int row, int column,
+                                               float bs) {
+  float value = static_cast<float>(sh.code[column * kCodeStride + row]) / 127.0f *
+                sh.smoothing[row] * sh.scales[column] * bs;
+  for (int r = 0; r < kRank; ++r) {
+    value += sh.ck[row * kRank + r] * sh.cv[column * kRank + r] * bs;
+    value -= sh.nk[row * kRank + r] * sh.nv[column * kRank + r];
+  }
+  for (int j = 0; j < kWindow; ++j) {
+    value += sh.rk[j * kDim + row] * sh.rc[j * kDim + column] * sh.record_suffix[j];
+  }
+  return value;
+}
+
+__global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
+  extern __shared__ __align__(16) unsigned char dynamic[];
+  PowerShared& sh = *reinterpret_cast<PowerShared*>(dynamic);
+  const int t = threadIdx.x;
+  const uint64_t state = blockIdx.x;
+  if (a.positions[state * kPositionStride] != static_cast<uint32_t>(kWindow)) return;  // uniform
+  const uint64_t vb = state * kDim;
+  const uint64_t rb = state * kWindow;
+
+  // ---- stage the state in LDS -----------------------------------------------
+  for (int i = t; i < kTile / 4; i += kThreads) {
+    const uint32_t w = reinterpret_cast<const uint32_t*>(a.residual + state * kTile)[i];
+    const int column = (4 * i) / kDim, row = (4 * i) % kDim;
+    *reinterpret_cast<uint32_t*>(&sh.code[column * kCodeStride + row]) = w;
+  }
+  for (int i = t; i < kDim * kRank; i += kThreads) {
+    sh.ck[i] = h2f(a.comp_keys[vb * kRank + i]);
+    sh.cv[i] = h2f(a.comp_values[vb * kRank + i]);
+    sh.nk[i] = 0.0f;
+    sh.nv[i] = 0.0f;
+  }
+  for (int i = t; i < kWindow * kDim; i += kThreads) {
+    sh.rk[i] = h2f(a.record_keys[rb * kDim + i]);
+    sh.rc[i] = h2f(a.record_corrections[rb * kDim + i]);
+  }
+  sh.smoothing[t] = a.smoothing[vb + t];
+  sh.scales[t] = a.scales[vb + t];
+  // BuildSuffix (:102-111), computed identically by every thread.
+  float bs = 1.0f;
+  for (int j = kWindow - 1; j >= 0; --j) {
+    if (t == 0) sh.record_suffix[j] = bs;
+    bs *= a.record_decay[rb + j];
+  }
+  __syncthreads();
+
+  // ---- deflated power iteration ---------------------------------------------
+  for (int rank = 0; rank < kRank; ++rank) {
+    sh.right[t] = static_cast<float>(static_cast<int>(((rank + 1) * (t + 3)) % 17) - 8);
+    __syncthreads();
+    (void)normalize(sh, sh.right, t);
+    for (uint32_t it = 0; it < a.power_iterations; ++it) {
+      apply_right(sh, sh.right, sh.left, bs, rank, t);
+      if (!normalize(sh, sh.left, t)) break;
+      apply_transpose(sh, sh.left, sh.right, bs, rank, t);
+      if (!normalize(sh, sh.right, t)) break;
+    }
+    apply_right(sh, sh.right, sh.left, bs, rank, t);
+    if (t == 0) {
+      float squared = 0.0f;
+      for (int i = 0; i < kDim; ++i) squared += sh.left[i] * sh.left[i];
+      sh.scalar = newton_sqrt(squared);
+    }
+    __syncthreads();
+    const float singular = sh.scalar;
+    if (singular > 1.0e-20f) {
+      const float inverse = 1.0f / singular;
+      sh.nk[t * kRank + rank] = round_half(sh.left[t] * inverse * singular);
+      sh.nv[t * kRank + rank] = round_half(sh.right[t]);
+    }
+    __syncthreads();
+  }
+
+  // ---- residual, fresh smoothing (row t), workspace ---------------------------
+  {
+    const int row = t;
+    float mean_absolute = 0.0f;
+    float* work = a.workspace + state * kTile + static_cast<uint64_t>(row) * kDim;
+    for (int column = 0; column < kDim; ++column) {
+      const float value = residual_cell(sh, row, column, bs);
+      work[column] = value;
+      mean_absolute += fabsf(value);
+    }
+    const float mean = mean_absolute / 128.0f;
+    const float s = newton_sqrt(mean > kBoundaryFloor ? mean : kBoundaryFloor);
+    sh.next_smoothing[row] = s;
+    a.next_smoothing[vb + row] = s;
+  }
+  __syncthreads();
+
+  // ---- scales and codes (column t) ------------------------------------------
+  {
+    const int column = t;
+    float maximum = 0.0f;
+    for (int row = 0; row < kDim; ++row) {
+      const float value = fabsf(residual_cell(sh, row, column, bs) / sh.next_smoothing[row]);
+      maximum = value > maximum ? value : maximum;
+    }
+    a.next_scales[vb + column] = maximum;
+    int8_t* out = a.next_residual + state * kTile + static_cast<uint64_t>(column) * kDim;
+    for (int row4 = 0; row4 < kDim; row4 += 4) {
+      uint32_t packed = 0;
+      for (int i = 0; i < 4; ++i) {
+        const float smoothed = residual_cell(sh, row4 + i, column, bs) / sh.next_smoothing[row4 + i];
+        float q = maximum == 0.0f ? 0.0f : smoothed / maximum * 127.0f;
+        q += q >= 0.0f ? 0.5f : -0.5f;
+        q = q > 127.0f ? 127.0f : q;
+        q = q < -127.0f ? -127.0f : q;
+        packed |= (static_cast<uint32_t>(static_cast<int>(q)) & 0xFFu) << (8 * i);
+      }
+      *reinterpret_cast<uint32_t*>(out + row4) = packed;
+    }
+  }
+
+  // ---- new compensators, cleared window, position ----------------------------
+  for (int i = t; i < kDim * kRank; i += kThreads) {
+    a.next_comp_keys[vb * kRank + i] = static_cast<uint16_t>(float_to_half_bits(sh.nk[i]));
+    a.next_comp_values[vb * kRank + i] = static_cast<uint16_t>(float_to_half_bits(sh.nv[i]));
+  }
+  for (int i = t; i < kWindow * kDim / 2; i += kThreads) {
+    reinterpret_cast<uint32_t*>(a.record_keys + rb * kDim)[i] = 0u;
+    reinterpret_cast<uint32_t*>(a.record_corrections + rb * kDim)[i] = 0u;
+  }
+  if (t < kWindow) a.record_decay[rb + t] = 0.0f;
+  __syncthreads();  // every thread has read the position word above
+  if (t == 0) a.positions[state * kPositionStride] = 0u;
+}
+
+}  // namespace
+
+int32_t launch_power_refit(void* stream, const int8_t* residual, const float* smoothing,
+                           const float* scales, const uint16_t* comp_keys,
+                           const uint16_t* comp_values, float* record_decay,
+                           uint16_t* record_keys, uint16_t* record_corrections,
+                           uint32_t* positions, int8_t* next_residual, float* next_smoothing,
+                           float* next_scales, uint16_t* next_comp_keys,
+                           uint16_t* next_comp_values, float* residual_workspace,
+                           uint32_t states, uint32_t power_iterations) {
+  const PowerArgs args{residual, smoothing, scales, comp_keys, comp_values, record_decay,
+                       record_keys, record_corrections, positions, next_residual, next_smoothing,
+                       next_scales, next_comp_keys, next_comp_values, residual_workspace,
+                       power_iterations};
+  void* pointers[] = {const_cast<PowerArgs*>(&args)};
+  const hipError_t status =
+      hipLaunchKernel(reinterpret_cast<const void*>(power_refit_kernel), dim3(states),
+                      dim3(kThreads), pointers, sizeof(PowerShared),
+                      static_cast<hipStream_t>(stream));
+  return status == hipSuccess ? kStatusOk : kStatusLaunchFailed;
+}
+
+}  // namespace gdn

@@ -56,12 +56,20 @@ SIGNATURES: dict[str, list] = {
     "statecentric_gdn_state_codec_int8_cube_matmul_launch_v1": [
         _P, _P, _P, _P, _U32, _U32, _P, _P, _U32],
     "statecentric_gdn_state_codec_decode_runtime_step_v1": [_P] * 17 + [_U32],
+    # window-boundary refit
+    "statecentric_gdn_state_codec_window_boundary_launch_v1": [_P] * 16 + [_U32, _U32],
+    "statecentric_gdn_state_codec_boundary_scale_records_launch_v1": [_P] * 4 + [_U32],
+    "statecentric_gdn_state_codec_window_boundary_cube_finish_launch_v1": [_P] * 16 + [_U32],
+    "statecentric_gdn_state_codec_bf16_cube_matmul_launch_v1": [_P] * 4 + [_U32, _P, _P, _U32],
+    "statecentric_gdn_state_codec_boundary_runtime_step_v1": [_P] * 7 + [_U32],
 }
 
 # Entry points that do not return a status: name -> (argtypes, restype).
 OTHER_SIGNATURES: dict[str, tuple] = {
     "statecentric_gdn_state_codec_decode_runtime_create_v1": ([_U32], _P),
     "statecentric_gdn_state_codec_decode_runtime_destroy_v1": ([_P], None),
+    "statecentric_gdn_state_codec_boundary_runtime_create_v1": ([_U32], _P),
+    "statecentric_gdn_state_codec_boundary_runtime_destroy_v1": ([_P], None),
 }
 
 

@@ -167,6 +167,73 @@ int32_t statecentric_gdn_state_codec_decode_runtime_step_v1(
     const uint16_t* queries, const uint16_t* values, uint16_t* outputs,
     uint32_t states);
 
+/* ---- window-boundary refit (kernel/gdn_state_codec_window_boundary.cpp) ---
+ * Boundaries are [value][key]; next_* buffers must not alias the inputs.
+ * All of these are bit-identical to the CPU statement of the reference
+ * kernels (with Axpy's product rounded before the add and the fp16 record
+ * GEMM summing in ascending record order). */
+
+/* power_iterations == 0: every state is re-encoded with its EXISTING smoothing
+ * from the dequantized boundary times the product S of its 16 record gates
+ * plus the 16 record terms key_j[k] * (corr_j[v] * suffix_j):
+ * m = w / s, scale' = max|m|, code' = rint_even(fp16(clamp(m * (127 / scale'))));
+ * next compensators are zero, records are kept, every position is reset to 0
+ * (the reference's finalize kernel).  power_iterations in 1..32: for each state
+ * at position 16, a deflated rank-4 power-iteration fit of the window's
+ * residual operator (stored as fp16 compensators), fresh smoothing
+ * sqrt(mean|row|) by 20 Newton steps, absmax scales, round-half-away codes,
+ * residual_workspace [S][key][value] receives the fitted residual, records are
+ * cleared and the position reset; states at other positions are untouched.
+ * 1 <= states <= 16384.  Replaces windowed_gdn_kernel.h:50-60
+ * (window_boundary.cpp:253-499, 653-696). */
+int32_t statecentric_gdn_state_codec_window_boundary_launch_v1(
+    void* stream, const int8_t* residual, const float* smoothing,
+    const float* scales, const uint16_t* compensator_keys,
+    const uint16_t* compensator_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    int8_t* next_residual, float* next_smoothing, float* next_scales,
+    uint16_t* next_compensator_keys, uint16_t* next_compensator_values,
+    float* residual_workspace, uint32_t states, uint32_t power_iterations);
+
+/* scaled_record_keys[s][j][k] = fp16(key_j[k] * fp16(prod_{i>j} gate_i)), the
+ * gate product taken in ascending order; 1 <= states <= 128.  Replaces
+ * windowed_gdn_kernel.h:62-67 (window_boundary.cpp:537-587, 698-712). */
+int32_t statecentric_gdn_state_codec_boundary_scale_records_launch_v1(
+    void* stream, const float* record_decay, const uint16_t* record_keys,
+    uint16_t* scaled_record_keys, uint32_t states);
+
+/* The quant-only refit above with the 16 record terms replaced by
+ * record_merge [S][value][key] fp32 (the boundary runtime's output);
+ * 1 <= states <= 128.  Replaces windowed_gdn_kernel.h:69-79
+ * (window_boundary.cpp:714-750). */
+int32_t statecentric_gdn_state_codec_window_boundary_cube_finish_launch_v1(
+    void* stream, const int8_t* residual, const float* smoothing,
+    const float* scales, const uint16_t* compensator_keys,
+    const uint16_t* compensator_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    int8_t* next_residual, float* next_smoothing, float* next_scales,
+    uint16_t* next_compensator_keys, uint16_t* next_compensator_values,
+    float* record_merge, uint32_t states);
+
+/* c[s] = a[s]^T b[s]: a, b fp16 [16][128], c fp32 [128][128], exact products
+ * summed in ascending k.  Admission as the reference (workspace and tiling
+ * non-null but unused, states <= 128, blocks == (states + 1) / 2).  Replaces
+ * windowed_gdn_kernel.h:81-84 (kernel/gdn_state_codec_bf16_cube_matmul.cpp:50-68). */
+int32_t statecentric_gdn_state_codec_bf16_cube_matmul_launch_v1(
+    void* stream, const uint16_t* a, const uint16_t* b, float* c, uint32_t states,
+    void* workspace, void* tiling, uint32_t blocks);
+
+/* Boundary runtime (host/gdn_state_codec_boundary_runtime.cpp:60-128): one
+ * process-wide reference-counted handle for 1..128 states; step scales the
+ * record keys then forms record_merge = corrections^T x scaled keys, returning
+ * 1 for a bad handle/pointer/count, 2 / 3 when the scaling / GEMM launch fails. */
+void* statecentric_gdn_state_codec_boundary_runtime_create_v1(uint32_t states);
+void statecentric_gdn_state_codec_boundary_runtime_destroy_v1(void* runtime);
+int32_t statecentric_gdn_state_codec_boundary_runtime_step_v1(
+    void* runtime, void* stream, const float* record_decay,
+    const uint16_t* record_keys, const uint16_t* record_corrections,
+    uint16_t* scaled_record_keys, float* record_merge, uint32_t states);
+
 #ifdef __cplusplus
 }
 #endif

@@ -264,6 +264,60 @@ void gdn_oracle_finish_decode_pair(
     const uint16_t* queries, const uint16_t* values, float* outputs,
     uint32_t states);
 
+/* ---- window-boundary refit (gdn_boundary_oracle.c) ------------------------
+ *
+ * Parity pins: statement-by-statement restatements of
+ * kernel/gdn_state_codec_window_boundary.cpp and bf16_cube_matmul.cpp; checked
+ * against the capsule semantics they approximate (the refit dense state equals
+ * DenseState of the window within the quantization error, the power
+ * iteration's first pair is the dominant singular pair of the closed-form
+ * residual operator computed independently in numpy) and the invariants of
+ * their output formats.  Two evaluation orders the reference leaves to the
+ * hardware are fixed: AscendC::Axpy is dst = src * s + dst with a rounded
+ * product, and the fp16 record-merge GEMM sums its 16 products in ascending k.
+ *
+ * Boundaries are [value][key] (the provider layout); records, compensators and
+ * positions as in the windowed step. */
+
+/* The 20-step Newton square root of window_boundary.cpp:17-23. */
+float gdn_oracle_boundary_sqrt(float value);
+
+/* window_boundary_launch_v1 with power_iterations == 0 (ProcessQuantOnlyTask,
+ * :368-499, plus the finalize kernel): every state is re-encoded with its
+ * existing smoothing from the dequantized boundary plus all 16 records
+ * (record_merge == NULL) or plus record_merge [S][value][key] fp32 (the
+ * window_boundary_cube_finish_launch_v1 form); compensator outputs are zero,
+ * records untouched, every position reset to 0. */
+void gdn_oracle_window_boundary_quant_only(
+    const int8_t* residual, const float* smoothing, const float* scales,
+    const float* record_decay, const uint16_t* record_keys,
+    const uint16_t* record_corrections, uint32_t* positions,
+    int8_t* next_residual, float* next_smoothing, float* next_scales,
+    uint16_t* next_comp_keys, uint16_t* next_comp_values,
+    const float* record_merge, uint32_t states);
+
+/* boundary_scale_records_launch_v1 (:537-587, 698-712). */
+void gdn_oracle_boundary_scale_records(const float* record_decay,
+                                       const uint16_t* record_keys,
+                                       uint16_t* scaled_record_keys,
+                                       uint32_t states);
+
+/* bf16_cube_matmul_launch_v1: C[s] = A[s]^T B[s], A and B fp16 [16][128]. */
+void gdn_oracle_f16_matmul_at_b(const uint16_t* a, const uint16_t* b, float* c,
+                                uint32_t states);
+
+/* window_boundary_launch_v1 with power_iterations in 1..32 (ProcessState,
+ * :253-366): for each state at position 16, a rank-4 power-iteration fit of
+ * the window's residual operator, re-encoding with fresh smoothing, records
+ * cleared and position reset; other states untouched. */
+void gdn_oracle_window_boundary_power(
+    const int8_t* residual, const float* smoothing, const float* scales,
+    const uint16_t* comp_keys, const uint16_t* comp_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    int8_t* next_residual, float* next_smoothing, float* next_scales,
+    uint16_t* next_comp_keys, uint16_t* next_comp_values,
+    float* residual_workspace, uint32_t states, uint32_t power_iterations);
+
 #ifdef __cplusplus
 }
 #endif

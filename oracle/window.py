@@ -288,3 +288,71 @@ def ref_read_window(codes, smoothing, scales, read, record_decay, record_keys,
         _ptr(out))
     assert status == 0
     return out
+
+
+# ------------------------------------------------------- window-boundary refit
+
+def _bind_boundary(l):
+    if getattr(l, "_boundary_bound", False):
+        return l
+    l.gdn_oracle_boundary_sqrt.argtypes = [ctypes.c_float]
+    l.gdn_oracle_boundary_sqrt.restype = ctypes.c_float
+    l.gdn_oracle_window_boundary_quant_only.argtypes = [_P] * 13 + [_U32]
+    l.gdn_oracle_window_boundary_quant_only.restype = None
+    l.gdn_oracle_boundary_scale_records.argtypes = [_P] * 3 + [_U32]
+    l.gdn_oracle_boundary_scale_records.restype = None
+    l.gdn_oracle_f16_matmul_at_b.argtypes = [_P] * 3 + [_U32]
+    l.gdn_oracle_f16_matmul_at_b.restype = None
+    l.gdn_oracle_window_boundary_power.argtypes = [_P] * 15 + [_U32, _U32]
+    l.gdn_oracle_window_boundary_power.restype = None
+    l._boundary_bound = True
+    return l
+
+
+def boundary_outputs(states: int) -> dict:
+    """Zeroed next-boundary buffers of a refit."""
+    return {"next_residual": np.zeros((states, DIM, DIM), np.int8),
+            "next_smoothing": np.zeros((states, DIM), np.float32),
+            "next_scales": np.zeros((states, DIM), np.float32),
+            "next_compensator_keys": np.zeros((states, DIM, RANK), np.uint16),
+            "next_compensator_values": np.zeros((states, DIM, RANK), np.uint16)}
+
+
+def window_boundary_quant_only(buf: dict, out: dict, record_merge=None) -> None:
+    """The quant-only refit; updates ``out`` and ``buf['positions']`` in place."""
+    states = buf["residual"].shape[0]
+    _bind_boundary(_l()).gdn_oracle_window_boundary_quant_only(
+        _ptr(buf["residual"]), _ptr(buf["smoothing"]), _ptr(buf["scales"]),
+        _ptr(buf["record_decay"]), _ptr(buf["record_keys"]), _ptr(buf["record_corrections"]),
+        _ptr(buf["positions"]), _ptr(out["next_residual"]), _ptr(out["next_smoothing"]),
+        _ptr(out["next_scales"]), _ptr(out["next_compensator_keys"]),
+        _ptr(out["next_compensator_values"]), _ptr(_c(record_merge, np.float32)), states)
+
+
+def boundary_scale_records(record_decay, record_keys):
+    states = record_decay.shape[0]
+    scaled = np.zeros((states, WINDOW, DIM), np.uint16)
+    _bind_boundary(_l()).gdn_oracle_boundary_scale_records(
+        _ptr(_c(record_decay, np.float32)), _ptr(_c(record_keys, np.uint16)), _ptr(scaled), states)
+    return scaled
+
+
+def f16_matmul_at_b(a, b):
+    states = a.shape[0]
+    c = np.zeros((states, DIM, DIM), np.float32)
+    _bind_boundary(_l()).gdn_oracle_f16_matmul_at_b(
+        _ptr(_c(a, np.uint16)), _ptr(_c(b, np.uint16)), _ptr(c), states)
+    return c
+
+
+def window_boundary_power(buf: dict, out: dict, workspace, power_iterations: int) -> None:
+    """The rank-4 power-iteration refit; updates ``out``, ``workspace`` and the
+    record/position arrays of ``buf`` in place."""
+    states = buf["residual"].shape[0]
+    _bind_boundary(_l()).gdn_oracle_window_boundary_power(
+        _ptr(buf["residual"]), _ptr(buf["smoothing"]), _ptr(buf["scales"]),
+        _ptr(buf["compensator_keys"]), _ptr(buf["compensator_values"]),
+        _ptr(buf["record_decay"]), _ptr(buf["record_keys"]), _ptr(buf["record_corrections"]),
+        _ptr(buf["positions"]), _ptr(out["next_residual"]), _ptr(out["next_smoothing"]),
+        _ptr(out["next_scales"]), _ptr(out["next_compensator_keys"]),
+        _ptr(out["next_compensator_values"]), _ptr(workspace), states, power_iterations)

@@ -149,3 +149,40 @@ def test_decode_runtime_lifecycle(lib):
     b = lib.decode_runtime_create_v1(32)  # released: a new count is accepted
     assert b
     lib.decode_runtime_destroy_v1(b)
+
+
+def test_boundary_entry_points_admit_like_the_reference(lib):
+    """window_boundary.cpp:661-669, 705-712, 724-731; bf16_cube_matmul.cpp:56-60."""
+    p = ctypes.c_void_p(16)
+    assert lib.window_boundary_launch_v1(None, *([p] * 15), 8, 33) == 1
+    for states in (0, 16385):
+        assert lib.window_boundary_launch_v1(None, *([p] * 15), states, 0) == 1
+    for i in range(15):
+        args = [p] * 15
+        args[i] = None
+        assert lib.window_boundary_launch_v1(None, *args, 8, 0) == 1
+        assert lib.window_boundary_cube_finish_launch_v1(None, *args, 8) == 1
+    for states in (0, 129):
+        assert lib.window_boundary_cube_finish_launch_v1(None, *([p] * 15), states) == 1
+        assert lib.boundary_scale_records_launch_v1(None, p, p, p, states) == 1
+    assert lib.bf16_cube_matmul_launch_v1(None, p, p, p, 8, p, p, 3) == 1
+    assert lib.bf16_cube_matmul_launch_v1(None, p, p, p, 8, None, p, 4) == 1
+    assert lib.bf16_cube_matmul_launch_v1(None, p, p, p, 130, p, p, 65) == 1
+
+
+def test_boundary_runtime_lifecycle(lib):
+    """boundary_runtime.cpp:60-128."""
+    p = ctypes.c_void_p(16)
+    assert not lib.boundary_runtime_create_v1(0)
+    assert not lib.boundary_runtime_create_v1(129)
+    a = lib.boundary_runtime_create_v1(32)
+    assert a and lib.boundary_runtime_create_v1(32) == a
+    assert not lib.boundary_runtime_create_v1(16)
+    assert lib.boundary_runtime_step_v1(a, None, p, p, p, p, p, 16) == 1
+    assert lib.boundary_runtime_step_v1(p, None, p, p, p, p, p, 32) == 1
+    assert lib.boundary_runtime_step_v1(a, None, p, None, p, p, p, 32) == 1
+    lib.boundary_runtime_destroy_v1(a)
+    lib.boundary_runtime_destroy_v1(a)
+    b = lib.boundary_runtime_create_v1(16)
+    assert b
+    lib.boundary_runtime_destroy_v1(b)

@@ -1,0 +1,130 @@
+"""GPU parity of the window-boundary refit (include/gdn_state_codec_window.h)
+against the oracle (oracle/gdn_boundary_oracle.c), through the C-ABI: every
+output bit-exact -- next boundary, smoothing, scales, compensators, workspace,
+records and positions -- and untouched buffers untouched."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import windowgen as WG
+from gdn_state_codec import native
+from oracle import window as W
+from test_window_gpu import dev, from_device, stream, to_device, window_ptrs
+
+pytestmark = pytest.mark.gpu
+
+VK = oracle.LAYOUT_VALUE_KEY
+OUT_NAMES = ("next_residual", "next_smoothing", "next_scales", "next_compensator_keys",
+             "next_compensator_values")
+
+
+def sentinel_outputs(states):
+    out = W.boundary_outputs(states)
+    out["next_residual"][:] = 0x5A
+    out["next_smoothing"][:] = -3.0
+    out["next_scales"][:] = -5.0
+    out["next_compensator_keys"][:] = 0x1234
+    out["next_compensator_values"][:] = 0x4321
+    return out
+
+
+def out_ptrs(d):
+    return [d[k].data_ptr() for k in OUT_NAMES]
+
+
+def assert_same(got: dict, want: dict, names):
+    for name in names:
+        assert got[name].tobytes() == want[name].tobytes(), name
+
+
+def test_quant_only_refit_is_bit_exact(device):
+    states = 384
+    print(f"quant-only refit states={states}", flush=True)
+    buf = WG.window_buffers(states, 61, VK, positions=(list(range(17)) * 23)[:states])
+    out = sentinel_outputs(states)
+    d, do = to_device(buf, device), to_device(out, device)
+    workspace = torch.zeros(16, dtype=torch.float32, device=device)
+    assert native().window_boundary_launch_v1(
+        stream(), *window_ptrs(d), *out_ptrs(do), workspace.data_ptr(), states, 0) == 0
+    torch.cuda.synchronize()
+    ref, ref_out = WG.copy_buffers(buf), WG.copy_buffers(out)
+    W.window_boundary_quant_only(ref, ref_out)
+    assert_same(from_device(do, out), ref_out, OUT_NAMES)
+    assert_same(from_device(d, buf), ref, buf.keys())
+
+
+def test_boundary_runtime_and_cube_finish_are_bit_exact(device):
+    states = 32
+    print(f"boundary runtime + cube finish states={states}", flush=True)
+    buf = WG.window_buffers(states, 63, VK, positions=16)
+    out = sentinel_outputs(states)
+    d, do = to_device(buf, device), to_device(out, device)
+    scaled = torch.zeros((states, 16, 128), dtype=torch.int16, device=device)
+    merge = torch.zeros((states, 128, 128), dtype=torch.float32, device=device)
+    lib = native()
+    handle = lib.boundary_runtime_create_v1(states)
+    assert handle
+    try:
+        assert lib.boundary_runtime_step_v1(
+            handle, stream(), d["record_decay"].data_ptr(), d["record_keys"].data_ptr(),
+            d["record_corrections"].data_ptr(), scaled.data_ptr(), merge.data_ptr(), states) == 0
+    finally:
+        lib.boundary_runtime_destroy_v1(handle)
+    assert lib.window_boundary_cube_finish_launch_v1(
+        stream(), *window_ptrs(d), *out_ptrs(do), merge.data_ptr(), states) == 0
+    torch.cuda.synchronize()
+    scaled_ref = W.boundary_scale_records(buf["record_decay"], buf["record_keys"])
+    merge_ref = W.f16_matmul_at_b(buf["record_corrections"], scaled_ref)
+    assert np.array_equal(scaled.cpu().numpy().view(np.uint16), scaled_ref)
+    assert merge.cpu().numpy().tobytes() == merge_ref.tobytes()
+    ref, ref_out = WG.copy_buffers(buf), WG.copy_buffers(out)
+    W.window_boundary_quant_only(ref, ref_out, merge_ref)
+    assert_same(from_device(do, out), ref_out, OUT_NAMES)
+    assert_same(from_device(d, buf), ref, buf.keys())
+
+
+def test_scale_records_and_record_gemm_entry_points(device):
+    states = 128
+    print("scale_records + bf16_cube_matmul", flush=True)
+    buf = WG.window_buffers(states, 65, VK, positions=16)
+    d = to_device(buf, device)
+    scaled = torch.zeros((states, 16, 128), dtype=torch.int16, device=device)
+    assert native().boundary_scale_records_launch_v1(
+        stream(), d["record_decay"].data_ptr(), d["record_keys"].data_ptr(), scaled.data_ptr(),
+        states) == 0
+    c = torch.zeros((states, 128, 128), dtype=torch.float32, device=device)
+    ws = torch.zeros(16, dtype=torch.int32, device=device)
+    assert native().bf16_cube_matmul_launch_v1(
+        stream(), d["record_corrections"].data_ptr(), scaled.data_ptr(), c.data_ptr(), states,
+        ws.data_ptr(), ws.data_ptr(), states // 2) == 0
+    torch.cuda.synchronize()
+    scaled_ref = W.boundary_scale_records(buf["record_decay"], buf["record_keys"])
+    assert np.array_equal(scaled.cpu().numpy().view(np.uint16), scaled_ref)
+    assert c.cpu().numpy().tobytes() == W.f16_matmul_at_b(buf["record_corrections"],
+                                                          scaled_ref).tobytes()
+
+
+@pytest.mark.parametrize("iterations", [1, 5, 32])
+def test_power_refit_is_bit_exact(device, iterations):
+    states = 10
+    print(f"power refit iterations={iterations}", flush=True)
+    from test_boundary_oracle import planted_window
+
+    buf = planted_window(states, 67)
+    buf["positions"][[2, 7], 0] = [5, 15]  # not full: untouched
+    out = sentinel_outputs(states)
+    workspace = np.full((states, 128, 128), 7.0, np.float32)
+    d, do = to_device(buf, device), to_device(out, device)
+    dw = dev(workspace, device)
+    assert native().window_boundary_launch_v1(
+        stream(), *window_ptrs(d), *out_ptrs(do), dw.data_ptr(), states, iterations) == 0
+    torch.cuda.synchronize()
+    ref, ref_out, ref_ws = WG.copy_buffers(buf), WG.copy_buffers(out), workspace.copy()
+    W.window_boundary_power(ref, ref_out, ref_ws, iterations)
+    assert_same(from_device(do, out), ref_out, OUT_NAMES)
+    assert_same(from_device(d, buf), ref, buf.keys())
+    assert dw.cpu().numpy().tobytes() == ref_ws.tobytes()
