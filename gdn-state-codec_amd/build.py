@@ -36,6 +36,12 @@ REFERENCE_LIBRARY_NAMES = (
     "libstatecentric_gdn_state_codec_dequantize_kernel.so",
     "libstatecentric_gdn_state_codec_provider_runtime.so",
     "libstatecentric_gdn_state_codec_encoded_projection_kernel.so",
+    "libstatecentric_gdn_state_codec_windowed_gdn_step_kernel.so",
+    "libstatecentric_gdn_state_codec_window_boundary_kernel.so",
+    "libstatecentric_gdn_state_codec_bf16_cube_matmul_kernel.so",
+    "libstatecentric_gdn_state_codec_int8_cube_matmul_kernel.so",
+    "libstatecentric_gdn_state_codec_boundary_runtime.so",
+    "libstatecentric_gdn_state_codec_decode_runtime.so",
 )
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -58,7 +58,7 @@ struct RefitArgs {
 
 // rint_even(fp16(t)): the Ascend cast to half, then to int8 with CAST_RINT.
 __device__ __forceinline__ uint32_t rint_through_half(float t) {
-  const float h = static_cast<float>(static_cast<_Float16>(t));
+  const float h = half_bits_to_float(float_to_half_bits(t));
   return static_cast<uint32_t>(static_cast<int32_t>(__builtin_rintf(h))) & 0xFFu;
 }
 

@@ -30,8 +30,13 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 }
 
-// Round to nearest even (v_cvt_f16_f32), with fp16 subnormals.
+// Round an fp32 value to nearest even fp16 (v_cvt_f16_f32), with fp16
+// subnormals. The empty asm pins `value` as a rounded fp32 register:
+// without it the compiler folds a producing multiply into v_fma_mixlo_f16,
+// which rounds the exact product once to fp16 and differs from rounding the
+// fp32 product at fp16 ties.
 __device__ __forceinline__ uint32_t float_to_half_bits(float value) {
+  asm volatile("" : "+v"(value));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(value));
 }
 

@@ -1,5 +1,6 @@
 """MI355X (gfx950) GDN state codec: int8 codec of Qwen3.5 gated-delta-net
-recurrent-state head tiles and the encoded projection, behind the reference's
+recurrent-state head tiles, the encoded projection, the windowed decode step
+and its window-boundary refit, behind the reference's
 ``statecentric_gdn_state_codec_*`` C-ABI."""
 
 from ._native import NativeLibrary, library_dir, library_path, native
@@ -13,12 +14,16 @@ from .codec import (
     project_chunked,
     project_decode,
 )
-from .runtime import GdnStateCodecRuntime
+from .runtime import GdnStateCodecExperiment, GdnStateCodecRuntime
+from .window import DecodeRuntime, WindowSlot
 
 __all__ = [
     "LAYOUT_KEY_VALUE",
     "LAYOUT_VALUE_KEY",
+    "DecodeRuntime",
+    "GdnStateCodecExperiment",
     "GdnStateCodecRuntime",
+    "WindowSlot",
     "NativeLibrary",
     "decode",
     "encode",

@@ -40,6 +40,7 @@ def test_slot_encode_reconstruct_and_project(device, heads):
     assert (np.abs(out[0] - out64) <= 2.0 ** -15 * bound + 1e-30).all()
     runtime.invalidate((1,))
     assert runtime._slot(state, 1) is not slot
+    runtime.close()
 
 
 def test_runtime_contract_errors(device):
@@ -56,3 +57,87 @@ def test_runtime_contract_errors(device):
         runtime.project(slot, torch.zeros((1, 1, 4, 128), dtype=torch.bfloat16, device=device))
     runtime.fall_back_to_native("multi-request decode batch")
     assert runtime.native_fallbacks == 1 and not runtime._slots
+    runtime.close()
+
+
+def slot_buffers(slot) -> dict:
+    """Host copy of a slot in the oracle's buffer naming."""
+    torch.cuda.synchronize()
+    h = lambda t, dt: t.cpu().numpy().view(dt).copy()  # noqa: E731
+    return {"residual": h(slot.residual, np.int8), "smoothing": h(slot.smoothing, np.float32),
+            "scales": h(slot.scales, np.float32),
+            "compensator_keys": h(slot.compensator_keys, np.uint16),
+            "compensator_values": h(slot.compensator_values, np.uint16),
+            "record_decay": h(slot.record_decay, np.float32),
+            "record_keys": h(slot.record_keys, np.uint16),
+            "record_corrections": h(slot.record_corrections, np.uint16),
+            "positions": h(slot.positions, np.uint32)}
+
+
+@pytest.mark.parametrize("backend,power", [("vector", 0), ("cube", 0), ("vector", 3)])
+def test_runtime_steps_through_two_window_refits(device, backend, power):
+    """40 decode tokens through GdnStateCodecRuntime.step (two refits): every
+    step and refit is checked against the oracle applied to the slot's own
+    buffers just before it."""
+    from gdn_state_codec import GdnStateCodecExperiment
+    from oracle import window as W
+    import windowgen as WG
+    from test_window_gpu import check_step
+
+    print(f"runtime steps backend={backend} power={power}", flush=True)
+    heads = 32
+    runtime = GdnStateCodecRuntime(GdnStateCodecExperiment(
+        decode_backend=backend, boundary_power_iterations=power))
+    provider = datagen.c1_heads(2 * heads, 9).reshape(2, heads, 128, 128)
+    state = torch.from_numpy(provider).to(device)
+    slot = runtime._slot(state, 1)
+    try:
+        for t in range(40):
+            inp = WG.bf16_inputs(heads, 300 + t)
+            before = slot_buffers(slot)
+            steps = slot.steps
+            if steps == 16:
+                out = W.boundary_outputs(heads)
+                if power == 0:
+                    scaled = W.boundary_scale_records(before["record_decay"], before["record_keys"])
+                    merge = W.f16_matmul_at_b(before["record_corrections"], scaled)
+                    W.window_boundary_quant_only(before, out, merge)
+                else:
+                    W.window_boundary_power(before, out, np.zeros((heads, 128, 128), np.float32),
+                                            power)
+                before.update(residual=out["next_residual"], smoothing=out["next_smoothing"],
+                              scales=out["next_scales"],
+                              compensator_keys=out["next_compensator_keys"],
+                              compensator_values=out["next_compensator_values"])
+            as_torch = lambda a, shape: torch.from_numpy(a.reshape(shape)).to(device)  # noqa
+            got = runtime.step(
+                state, 1,
+                as_torch(inp["queries"].view(np.int16), (1, 1, heads // 2, 128)).view(torch.bfloat16),
+                as_torch(inp["keys"].view(np.int16), (1, 1, heads // 2, 128)).view(torch.bfloat16),
+                as_torch(inp["values"].view(np.int16), (1, 1, heads, 128)).view(torch.bfloat16),
+                as_torch(inp["log_decay"], (1, 1, heads)),
+                as_torch(inp["beta"].view(np.int16), (1, 1, heads)).view(torch.bfloat16),
+                128 ** -0.5)
+            after = slot_buffers(slot)
+            if steps == 16:  # the refit's new boundary, bit-exact
+                for name in ("residual", "smoothing", "scales", "compensator_keys",
+                             "compensator_values"):
+                    assert after[name].tobytes() == before[name].tobytes(), (t, name)
+            out_gpu = got.view(torch.int16).cpu().numpy().view(np.uint16).reshape(heads, 128)
+            ref = WG.copy_buffers(before)
+            if backend == "vector":
+                out_ref, out64, out_bound, corr64, corr_bound = W.windowed_step_bf16(
+                    ref, **inp, quant_only=power == 0)
+                check_step(before, after, ref, out_gpu, out_ref, out64, out_bound, corr64,
+                           corr_bound, 16)
+            else:
+                q, dyn = W.prepare_decode_pair_bf16(inp["keys"], inp["queries"],
+                                                    inp["log_decay"], before["smoothing"])
+                out_ref = W.finish_decode_pair_bf16(
+                    ref, W.int8_matmul(before["residual"], q), dyn, **inp)
+                assert out_gpu.tobytes() == out_ref.tobytes(), t
+                for name in ref:
+                    assert after[name].tobytes() == ref[name].tobytes(), (t, name)
+        assert runtime.boundary_refits == 2
+    finally:
+        runtime.close()
