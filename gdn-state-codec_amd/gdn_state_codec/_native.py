@@ -21,6 +21,7 @@ _U32 = ctypes.c_uint32
 _U64 = ctypes.c_uint64
 _F = ctypes.c_float
 _I32 = ctypes.c_int32
+_C = ctypes.c_char_p
 
 # name -> argtypes (all return int32 status)
 SIGNATURES: dict[str, list] = {
@@ -62,6 +63,11 @@ SIGNATURES: dict[str, list] = {
     "statecentric_gdn_state_codec_window_boundary_cube_finish_launch_v1": [_P] * 16 + [_U32],
     "statecentric_gdn_state_codec_bf16_cube_matmul_launch_v1": [_P] * 4 + [_U32, _P, _P, _U32],
     "statecentric_gdn_state_codec_boundary_runtime_step_v1": [_P] * 7 + [_U32],
+    # include/gdn_state_codec_capsule.h
+    "statecentric_gdn_state_codec_capsule_serialize_launch_v1":
+        [_P] * 10 + [_U32, _C, _U64, _U64, _P, _P, _U64, _P, _U32],
+    "statecentric_gdn_state_codec_capsule_restore_launch_v1":
+        [_P] * 4 + [_U64, _C, _U64, _U64, _P, _U32] + [_P] * 10 + [_U32],
 }
 
 # Entry points that do not return a status: name -> (argtypes, restype).
@@ -70,6 +76,7 @@ OTHER_SIGNATURES: dict[str, tuple] = {
     "statecentric_gdn_state_codec_decode_runtime_destroy_v1": ([_P], None),
     "statecentric_gdn_state_codec_boundary_runtime_create_v1": ([_U32], _P),
     "statecentric_gdn_state_codec_boundary_runtime_destroy_v1": ([_P], None),
+    "statecentric_gdn_state_codec_capsule_bytes_v1": ([_U32], _U64),
 }
 
 

@@ -318,6 +318,77 @@ void gdn_oracle_window_boundary_power(
     uint16_t* next_comp_keys, uint16_t* next_comp_values,
     float* residual_workspace, uint32_t states, uint32_t power_iterations);
 
+/* ---- capsule wire format LQCAPS01 (gdn_capsule_oracle.c) ------------------
+ *
+ * Parity pins: SHA-256 vs FIPS 180-4 vectors, hashlib and the reference's
+ * Sha256Hex; serialize / restore vs the reference's Serialize / Restore
+ * (oracle/_ref) on reference-built capsules, the reference test's corruptions
+ * and slot capsules (see the header of gdn_capsule_oracle.c). */
+
+/* Restore outcomes, one per check of GdnStateCodecCapsule::Restore
+ * (state_capsule.cpp:476-578) in the order the reference makes them. */
+#define GDN_ORACLE_CAPSULE_OK 0
+#define GDN_ORACLE_CAPSULE_TRUNCATED 1          /* too short / truncated field */
+#define GDN_ORACLE_CAPSULE_MAGIC 2
+#define GDN_ORACLE_CAPSULE_DIGEST_ENCODING 3    /* digest not lowercase hex */
+#define GDN_ORACLE_CAPSULE_DIGEST_MISMATCH 4
+#define GDN_ORACLE_CAPSULE_PARAMETERS 5
+#define GDN_ORACLE_CAPSULE_IDENTITY 6
+#define GDN_ORACLE_CAPSULE_RANK 7
+#define GDN_ORACLE_CAPSULE_POSITION 8           /* window position >= window */
+#define GDN_ORACLE_CAPSULE_PHASE 9              /* position != expected */
+#define GDN_ORACLE_CAPSULE_RESIDUAL_DOMAIN 10   /* a code equals -128 */
+#define GDN_ORACLE_CAPSULE_BOUNDARY_PAYLOAD 11
+#define GDN_ORACLE_CAPSULE_RECORD_NONFINITE 12
+#define GDN_ORACLE_CAPSULE_TRAILING 13
+#define GDN_ORACLE_CAPSULE_STATE_NONFINITE 14
+#define GDN_ORACLE_CAPSULE_DEVICE_FORMAT 15     /* slot restore only */
+#define GDN_ORACLE_CAPSULE_ARGUMENT 17          /* expected identity/parameters invalid */
+
+void gdn_oracle_sha256(const uint8_t* data, uint64_t size, uint8_t digest[32]);
+void gdn_oracle_sha256_hex(const uint8_t* data, uint64_t size, char hex[64]);
+
+/* Encoded size: header 120 + codes + fp32 smoothing, scales, compensators and
+ * records + 64 digest characters. */
+uint64_t gdn_oracle_capsule_bytes(uint32_t keys, uint32_t values, uint32_t rank,
+                                  uint32_t updates);
+
+/* Serialize (state_capsule.cpp:446-474); returns the byte count. */
+uint64_t gdn_oracle_capsule_serialize(
+    const char* geometry, uint64_t generation, uint64_t epoch, uint32_t keys,
+    uint32_t values, uint32_t schema, uint32_t window, uint32_t rank, uint32_t bits,
+    float smoothing_floor, const int8_t* residual, const float* smoothing,
+    const float* scales, const float* comp_keys, const float* comp_values,
+    uint32_t updates, const float* decay, const float* key, const float* correction,
+    uint8_t* out);
+
+/* Restore (state_capsule.cpp:476-578): a GDN_ORACLE_CAPSULE_* outcome; the
+ * fields are complete only on success.  dense_work holds keys*values floats. */
+int gdn_oracle_capsule_restore(
+    const uint8_t* encoded, uint64_t size, const char* geometry, uint64_t generation,
+    uint64_t epoch, uint32_t keys, uint32_t values, uint32_t schema, uint32_t window,
+    uint32_t rank, uint32_t bits, float smoothing_floor, uint32_t expected_position,
+    int8_t* residual, float* smoothing, float* scales, float* comp_keys,
+    float* comp_values, float* decay, float* key, float* correction,
+    float* dense_work, uint32_t* updates_out);
+
+/* One device window slot state (128x128, rank 4, window 16) as a capsule, and
+ * back.  serialize returns 0 for a position >= 16; restore writes the slot
+ * only on success and refuses (DEVICE_FORMAT) a capsule whose per-key decays
+ * differ within a record or whose compensators / records are not fp16. */
+uint64_t gdn_oracle_slot_capsule_bytes(uint32_t position);
+uint64_t gdn_oracle_slot_capsule_serialize(
+    uint32_t layout, const int8_t* residual, const float* smoothing, const float* scales,
+    const uint16_t* comp_keys, const uint16_t* comp_values, const float* record_decay,
+    const uint16_t* record_keys, const uint16_t* record_corrections, uint32_t position,
+    const char* geometry, uint64_t generation, uint64_t epoch, uint8_t* out);
+int gdn_oracle_slot_capsule_restore(
+    const uint8_t* encoded, uint64_t size, const char* geometry, uint64_t generation,
+    uint64_t epoch, uint32_t expected_position, uint32_t layout, int8_t* residual,
+    float* smoothing, float* scales, uint16_t* comp_keys, uint16_t* comp_values,
+    float* record_decay, uint16_t* record_keys, uint16_t* record_corrections,
+    uint32_t* position_word);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,7 +12,10 @@
 
 #include <cstdint>
 #include <cstring>
+#include <algorithm>
 #include <exception>
+#include <string>
+#include <string_view>
 #include <vector>
 
 #include "statecentric/gdn_state_codec_qwen38_gdn_adapter.h"
@@ -28,6 +31,23 @@ statecentric::GdnStateCodecParameters MakeParameters(std::uint32_t rank) {
   statecentric::GdnStateCodecParameters parameters;
   parameters.compensator_rank = rank;
   return parameters;
+}
+
+// Copies encoded capsule bytes out; 1 when `capacity` is too small.
+int CopyBytes(const std::vector<std::uint8_t>& bytes, std::uint8_t* out,
+              std::uint64_t capacity, std::uint64_t* size) {
+  *size = bytes.size();
+  if (bytes.size() > capacity) return 1;
+  std::memcpy(out, bytes.data(), bytes.size());
+  return 0;
+}
+
+// The exception text, NUL-terminated and cut to `capacity` bytes.
+void CopyMessage(const char* text, char* message, std::uint64_t capacity) {
+  if (message == nullptr || capacity == 0) return;
+  const std::size_t length = std::min<std::size_t>(std::strlen(text), capacity - 1);
+  std::memcpy(message, text, length);
+  message[length] = '\0';
 }
 
 }  // namespace
@@ -263,6 +283,91 @@ int gdnref_dequantize_heads(const std::int8_t* residual,
     if (status != 0) return status;
   }
   return 0;
+}
+
+// Sha256Hex (native/src/sha256.cpp): 64 lowercase hex characters of the
+// SHA-256 of `size` bytes.
+int gdnref_sha256_hex(const std::uint8_t* data, std::uint64_t size, char* hex) {
+  const std::string text = statecentric::Sha256Hex(
+      std::string_view(reinterpret_cast<const char*>(data), size));
+  std::memcpy(hex, text.data(), text.size());
+  return 0;
+}
+
+// A capsule the reference builds itself: FromDenseBoundary (rank 4) of a
+// [keys][values] state with identity (geometry, generation, epoch), ApplyToken
+// per token (inputs as in gdnref_apply_tokens), then Serialize
+// (state_capsule.cpp:446-474).  0 on success, 1 with `message` on an exception
+// or when `capacity` is too small.
+int gdnref_capsule_after_tokens(const float* dense, std::uint32_t keys,
+                                std::uint32_t values, std::uint32_t tokens,
+                                const float* decay, const float* key,
+                                const float* value, const float* read,
+                                const float* query, const char* geometry,
+                                std::uint64_t generation, std::uint64_t epoch,
+                                std::uint8_t* out, std::uint64_t capacity,
+                                std::uint64_t* size, char* message,
+                                std::uint64_t message_capacity) {
+  try {
+    statecentric::GdnStateCodecIdentity identity{std::string(geometry, 64),
+                                                 generation, epoch, keys, values};
+    auto capsule = statecentric::GdnStateCodecCapsule::FromDenseBoundary(
+        std::span<const float>(dense, std::size_t{keys} * values), identity,
+        MakeParameters(4));
+    for (std::uint32_t t = 0; t < tokens; ++t) {
+      statecentric::GdnStateCodecTokenInput input;
+      input.decay.assign(decay + std::size_t{t} * keys, decay + std::size_t{t + 1} * keys);
+      input.key.assign(key + std::size_t{t} * keys, key + std::size_t{t + 1} * keys);
+      input.read.assign(read + std::size_t{t} * keys, read + std::size_t{t + 1} * keys);
+      input.query.assign(query + std::size_t{t} * keys, query + std::size_t{t + 1} * keys);
+      input.value.assign(value + std::size_t{t} * values,
+                         value + std::size_t{t + 1} * values);
+      (void)capsule.ApplyToken(input);
+    }
+    if (CopyBytes(capsule.Serialize(), out, capacity, size) != 0) {
+      CopyMessage("output capacity too small", message, message_capacity);
+      return 1;
+    }
+    return 0;
+  } catch (const std::exception& error) {
+    CopyMessage(error.what(), message, message_capacity);
+    return 1;
+  }
+}
+
+// Restore (state_capsule.cpp:476-578) against the expected identity,
+// parameters and window position; on success the restored capsule's
+// Serialize() goes to `out` and its DenseState() ([keys][values]) to `dense`.
+// 0 on success, 1 with the exception's message on rejection.
+int gdnref_capsule_restore(const std::uint8_t* encoded, std::uint64_t size,
+                           const char* geometry, std::uint64_t generation,
+                           std::uint64_t epoch, std::uint32_t keys,
+                           std::uint32_t values, std::uint32_t schema,
+                           std::uint32_t window, std::uint32_t rank,
+                           std::uint32_t bits, float smoothing_floor,
+                           std::uint32_t expected_position, std::uint8_t* out,
+                           std::uint64_t capacity, std::uint64_t* out_size,
+                           float* dense, char* message,
+                           std::uint64_t message_capacity) {
+  try {
+    const statecentric::GdnStateCodecIdentity identity{
+        std::string(geometry, 64), generation, epoch, keys, values};
+    statecentric::GdnStateCodecParameters parameters{schema, window, rank, bits,
+                                                     smoothing_floor};
+    const auto restored = statecentric::GdnStateCodecCapsule::Restore(
+        std::span<const std::uint8_t>(encoded, size), identity, parameters,
+        expected_position);
+    if (CopyBytes(restored.Serialize(), out, capacity, out_size) != 0) {
+      CopyMessage("output capacity too small", message, message_capacity);
+      return 1;
+    }
+    const auto state = restored.DenseState();
+    std::memcpy(dense, state.data(), state.size() * sizeof(float));
+    return 0;
+  } catch (const std::exception& error) {
+    CopyMessage(error.what(), message, message_capacity);
+    return 1;
+  }
 }
 
 }  // extern "C"

@@ -186,3 +186,37 @@ def test_boundary_runtime_lifecycle(lib):
     b = lib.boundary_runtime_create_v1(16)
     assert b
     lib.boundary_runtime_destroy_v1(b)
+
+
+def test_capsule_entry_points_admit_and_size_capsules(lib):
+    """The capsule entry points reject before any HIP call: null pointers,
+    states outside 1..16384, layouts other than 0/1 and an identity that
+    ValidateIdentity refuses (state_capsule.cpp:40-48)."""
+    for p in range(16):
+        assert lib.capsule_bytes_v1(p) == 21688 + 1536 * p
+    assert lib.capsule_bytes_v1(16) == 0 and lib.capsule_bytes_v1(2 ** 32 - 1) == 0
+    p = ctypes.c_void_p(16)
+    good = b"0123456789abcdef" * 4
+
+    def ser(args=None, layout=1, geometry=good, generation=1, epoch=1, states=4):
+        args = [p] * 12 if args is None else args
+        return lib.capsule_serialize_launch_v1(None, *args[:9], layout, geometry, generation,
+                                               epoch, args[9], args[10], 1 << 20, args[11],
+                                               states)
+
+    def res(args=None, layout=1, geometry=good, generation=1, epoch=1, states=4):
+        args = [p] * 14 if args is None else args
+        return lib.capsule_restore_launch_v1(None, *args[:3], 1 << 20, geometry, generation,
+                                             epoch, args[3], layout, *args[4:], states)
+
+    for fn, n in ((ser, 12), (res, 14)):
+        for i in range(n):
+            args = [p] * n
+            args[i] = None
+            assert fn(args) == 1, (fn.__name__, i)
+        for states in (0, 16385):
+            assert fn(states=states) == 1
+        assert fn(layout=2) == 1
+        for geometry in (b"A" * 64, b"0123456789abcdeg" + b"0" * 48, None):
+            assert fn(geometry=geometry) == 1
+        assert fn(generation=0) == 1 and fn(epoch=0) == 1
