@@ -6,7 +6,9 @@ Headline workload: one step = quantize + dequantize of a
 (config 3) and the chunked projection 64 x T=64 x 32 heads (config 4), both
 rotating over 5 distinct state copies so the 256 MB Infinity Cache cannot hold
 the working set.  Kernel durations come from HIP events recorded on the stream
-the kernels are launched on (torch's current stream).
+the kernels are launched on (torch's current stream).  The windowed decode
+step, its capsule wire format (serialize / restore) and, with --pool, config 5
+are reported beside the headline line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--pool]
 
@@ -314,6 +316,121 @@ def bench_window_step(warmup: int):
     return results
 
 
+CAPSULE_GEOMETRY = "0123456789abcdef" * 4
+SHA_BLOCKS_PER_CAPSULE = lambda p: (21624 + 1536 * p + 9 + 63) // 64  # noqa: E731
+
+
+def capsule_slot(states: int, dev, seed: int = 11):
+    """A window slot of `states` random states; the 32 heads of a sequence
+    share one window position, sequences cycle through positions 0..15."""
+    import torch
+
+    from gdn_state_codec.window import WindowSlot
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    slot = WindowSlot.allocate(states, dev)
+    slot.residual.copy_(torch.randint(-127, 128, slot.residual.shape, device=dev, generator=gen,
+                                      dtype=torch.int8))
+    for t in (slot.smoothing, slot.scales, slot.record_decay):
+        t.uniform_(0.5, 1.5, generator=gen)
+    for t in (slot.compensator_keys, slot.compensator_values, slot.record_keys,
+              slot.record_corrections):
+        t.copy_((torch.randn(t.shape, device=dev, generator=gen) * 0.05).to(torch.float16))
+    slot.positions[:, 0] = (torch.arange(states, device=dev, dtype=torch.int32) // 32) % 16
+    return slot
+
+
+def bench_capsule(steps: int, warmup: int):
+    """Capsule wire format at B=256 (8192 states): serialize (pack + SHA-256)
+    and restore (SHA-256 verify + validate/unpack) of a whole slot batch."""
+    import torch
+
+    from gdn_state_codec import capsule as cap
+    from gdn_state_codec import native
+    from gdn_state_codec.window import WindowSlot
+
+    dev = torch.device("cuda:0")
+    states = WINDOW_STATES
+    slot = capsule_slot(states, dev)
+    fresh = WindowSlot.allocate(states, dev)
+    identity = cap.CapsuleIdentity(CAPSULE_GEOMETRY, 1, 1)
+    capsules, offsets, lengths = cap.serialize(slot, identity)
+    expected = slot.positions[:, 0].contiguous()
+    status = cap.restore(fresh, capsules, offsets, lengths, identity, expected)
+    torch.cuda.synchronize()
+    assert bool((status == 0).all()) and bool((lengths > 0).all())
+    lib, stream = native(), torch.cuda.current_stream().cuda_stream
+    geometry = identity.geometry_bytes
+
+    def serialize():
+        return lib.capsule_serialize_launch_v1(
+            stream, *slot.pointers(), 1, geometry, 1, 1, capsules.data_ptr(), offsets.data_ptr(),
+            capsules.numel(), lengths.data_ptr(), states)
+
+    def restore():
+        return lib.capsule_restore_launch_v1(
+            stream, capsules.data_ptr(), offsets.data_ptr(), lengths.data_ptr(), capsules.numel(),
+            geometry, 1, 1, expected.data_ptr(), 1, *fresh.pointers(), status.data_ptr(), states)
+
+    results = {}
+    capsule_bytes = int(lengths.sum().item())
+    positions = expected.cpu().tolist()
+    blocks = sum(SHA_BLOCKS_PER_CAPSULE(p) for p in positions)
+    for name, run in (("serialize", serialize), ("restore", restore)):
+        for _ in range(max(warmup, 1)):
+            assert run() == 0
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            run()
+        b.record()
+        us = _events_ms([(a, b)])[0] / steps * 1e3
+        results[name] = {"us_per_batch": us, "capsules_per_s": states / (us * 1e-6),
+                         "capsule_GBps": capsule_bytes / (us * 1e-6) / 1e9,
+                         "sha256_blocks_per_s": blocks / (us * 1e-6)}
+        _log(f"capsule {name}: {us:.1f} us for {states} capsules "
+             f"({results[name]['capsule_GBps']:.0f} GB/s of capsule bytes)")
+    assert bool((status == 0).all())
+    results["workload"] = ("LQCAPS01 serialize / restore of B=256 x 32 heads (8192 window "
+                           "states), sequence s at window position s mod 16")
+    results["capsule_bytes"] = capsule_bytes
+    results["sha256_blocks"] = blocks
+    results["capsules"] = states
+    del slot, fresh, capsules
+    return results
+
+
+def cpu_baseline_capsule(target_seconds: float = 6.0):
+    """Part of the cpu_baseline leg: the C restatement's slot serialize (one
+    thread) on a bounded sample of the bench_capsule batch."""
+    import numpy as np
+    import torch
+
+    from oracle import capsule as C
+
+    dev = torch.device("cuda:0")
+    slot = capsule_slot(WINDOW_STATES, dev)
+    names = ("residual", "smoothing", "scales", "compensator_keys", "compensator_values",
+             "record_decay", "record_keys", "record_corrections", "positions")
+    sample = 512
+    buf = {}
+    for n in names:
+        t = getattr(slot, n)[:sample].cpu()
+        buf[n] = t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.float16 else (
+            t.numpy().view(np.uint32) if n == "positions" else t.numpy())
+    identity = C.Identity(CAPSULE_GEOMETRY, 1, 1)
+    done, nbytes, t0 = 0, 0, time.perf_counter()
+    while done < sample and (done < 16 or time.perf_counter() - t0 < target_seconds):
+        nbytes += len(C.slot_serialize(buf, done, 1, identity))
+        done += 1
+    seconds = time.perf_counter() - t0
+    _log(f"cpu capsule serialize (port): {done} capsules in {seconds:.2f} s")
+    return {"capsules_per_s": done / seconds, "capsule_GBps": nbytes / seconds / 1e9,
+            "cores": 1, "kind": "port", "sample": f"{done} capsules of the bench batch"}
+
+
 def bench_pool(steps: int, warmup: int):
     """Config 5 with a bf16 pool (64.4 GB): gather-encode and decode-scatter."""
     import torch
@@ -424,6 +541,7 @@ def profile_pass() -> int:
     bench_decode_projection(1, 0)
     bench_chunked_projection(1, 0)
     bench_window_step(0)
+    bench_capsule(1, 0)
     torch.cuda.synchronize()
     print(json.dumps({"profile_pass": "done"}), flush=True)
     return 0
@@ -482,6 +600,10 @@ def main() -> int:
             "bytes_per_step": C4_BYTES, "rotated_state_copies": ROTATIONS}
         torch.cuda.empty_cache()
         extra["windowed_step"] = bench_window_step(args.warmup)
+        torch.cuda.empty_cache()
+        extra["capsule"] = bench_capsule(max(args.steps // 4, 3), args.warmup)
+        if not args.no_cpu:
+            extra["capsule"]["cpu_baseline"] = cpu_baseline_capsule()
     if args.pool:
         extra["pool_codec"] = bench_pool(max(args.steps // 4, 2), 1)
     line = {

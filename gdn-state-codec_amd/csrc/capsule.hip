@@ -19,6 +19,7 @@
 // issue, not HBM: one 64-byte block is ~1.5k VALU instructions.  The pack and
 // unpack kernels move 22-45 KB per state and are HBM-bound.
 #include <hip/hip_runtime.h>
+#include <float.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -442,6 +443,7 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
   __shared__ uint32_t header[kHeaderWords];
   __shared__ float sm[kDim], sc[kDim], ck[kDim * kRank], cv[kDim * kRank];
   __shared__ float rec[(kWindow - 1) * kRecordFloats];  // records 0..14
+  __shared__ float maxima[4 + 3 * (kWindow - 1)];
   __shared__ __align__(16) uint8_t tile[kDim * kTileStride];
   const uint32_t s = blockIdx.x;
   const int t = threadIdx.x;
@@ -549,25 +551,62 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
     if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_TRAILING;
     return;
   }
-  // DenseState (:337-352) must be finite, evaluated in its own order:
-  // ((s*code)/127)*scale, + ck.cv over the rank, then decay*x + key*corr per
-  // record (the build disables contraction, so no FMA forms).
+  // DenseState (:337-352) must be finite.  A magnitude bound decides it for
+  // almost every capsule: with B0 = max|s| max|scale| + 4 max|ck| max|cv| and
+  // Bj = max|decay_j| B(j-1) + max|key_j| max|corr_j|, every value the
+  // reference's fp32 evaluation forms after s*code is at most
+  // B_p (1 + 2^-24)^40 in magnitude, so B_p and max|s| * 127 below
+  // FLT_MAX (1 - 2^-10) prove the state finite.  Otherwise it is evaluated
+  // exactly, in its own order: ((s*code)/127)*scale, + ck.cv over the rank,
+  // then decay*x + key*corr per record (the build disables contraction).
+  {
+    const int wave = t >> 6, lane = t & 63;
+    // Vector 0 smoothing, 1 scales, 2 ck, 3 cv, 4 + 3j + {0, 1, 2} record j.
+    for (uint32_t vec = wave; vec < 4 + 3 * count; vec += kThreads / 64) {
+      float m = 0.0f;
+      if (vec < 2) {
+        const float* src = vec == 0 ? sm : sc;
+        m = fmaxf(fabsf(src[lane]), fabsf(src[lane + 64]));
+      } else if (vec < 4) {
+        const float* src = vec == 2 ? ck : cv;
+        for (int i = lane; i < kDim * kRank; i += 64) m = fmaxf(m, fabsf(src[i]));
+      } else {
+        const float* src = rec + (vec - 4) * kDim;
+        m = fmaxf(fabsf(src[lane]), fabsf(src[lane + 64]));
+      }
+      m = wave_max(m);
+      if (lane == 0) maxima[vec] = m;
+    }
+  }
+  __syncthreads();
+  double bound = static_cast<double>(maxima[0]) * maxima[1] +
+                 4.0 * static_cast<double>(maxima[2]) * maxima[3];
+  for (uint32_t j = 0; j < count; ++j) {
+    bound = static_cast<double>(maxima[4 + 3 * j]) * bound +
+            static_cast<double>(maxima[5 + 3 * j]) * maxima[6 + 3 * j];
+  }
+  const double limit = static_cast<double>(FLT_MAX) * (1.0 - 1.0 / 1024.0);
+  if (!(bound < limit && static_cast<double>(maxima[0]) * 127.0 < limit)) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int w = i * kThreads + t;
-    const int k = w >> 4, v0 = (w & 15) * 8;
+    for (int i = 0; i < 8; ++i) {
+      const int w = i * kThreads + t;
+      const int k = w >> 4, v0 = (w & 15) * 8;
+      float x[8];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const int v = v0 + b;
-      const float code = static_cast<float>(static_cast<int8_t>(codes[i] >> (8 * b)));
-      float x = sm[k] * code / 127.0f * sc[v];
+      for (int b = 0; b < 8; ++b) {
+        const float code = static_cast<float>(static_cast<int8_t>(codes[i] >> (8 * b)));
+        x[b] = sm[k] * code / 127.0f * sc[v0 + b];
 #pragma unroll
-      for (int r = 0; r < kRank; ++r) x += ck[k * kRank + r] * cv[v * kRank + r];
+        for (int r = 0; r < kRank; ++r) x[b] += ck[k * kRank + r] * cv[(v0 + b) * kRank + r];
+      }
       for (uint32_t j = 0; j < count; ++j) {
         const float* r = rec + j * kRecordFloats;
-        x = r[k] * x + r[kDim + k] * r[2 * kDim + v];
+        const float decay = r[k], key = r[kDim + k];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) x[b] = decay * x[b] + key * r[2 * kDim + v0 + b];
       }
-      bad = bad || !isfinite(x);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) bad = bad || !isfinite(x[b]);
     }
   }
   if (__syncthreads_or(bad)) {

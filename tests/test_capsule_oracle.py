@@ -202,6 +202,10 @@ def corruptions(encoded: bytes, keys: int, values: int, position: int):
          C.BOUNDARY_PAYLOAD),
         ("compensator nan", _patched(encoded, comps + 8, _f(np.nan)), IDENTITY, position,
          C.BOUNDARY_PAYLOAD),
+        # Finite, though s * 127 would overflow: only an exact evaluation of
+        # DenseState admits it.
+        ("large smoothing", _patched(_patched(encoded, residual, b"\x32" * values, False),
+                                     smoothing, _f(3.0e36)), IDENTITY, position, C.OK),
     ]
     if position:
         cases.append(("record inf", _patched(encoded, records + 4 * keys, _f(np.inf)),
