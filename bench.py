@@ -7,8 +7,8 @@ Headline workload: one step = quantize + dequantize of a
 rotating over 5 distinct state copies so the 256 MB Infinity Cache cannot hold
 the working set.  Kernel durations come from HIP events recorded on the stream
 the kernels are launched on (torch's current stream).  The windowed decode
-step, its capsule wire format (serialize / restore) and, with --pool, config 5
-are reported beside the headline line.
+step, its window-boundary refit, the capsule wire format (serialize /
+restore) and, with --pool, config 5 are reported beside the headline line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--pool]
 
@@ -316,6 +316,86 @@ def bench_window_step(warmup: int):
     return results
 
 
+REFIT_POWER_ITERATIONS = 4
+
+
+def refit_bytes(power: bool) -> int:
+    """Algorithmic HBM bytes of one window-boundary refit of one full window:
+    the boundary codes, smoothing and scales, the 16 records (gates, fp16 keys
+    and corrections) read; the next codes, smoothing, scales and compensators
+    and the position written.  The power refit also reads the compensators and
+    writes the fitted residual workspace (fp32 [128][128]) and the cleared
+    records."""
+    read = 128 * 128 + 2 * 128 * 4 + 16 * 4 + 2 * 16 * 128 * 2
+    write = 128 * 128 + 2 * 128 * 4 + 2 * 128 * 4 * 2 + 4
+    if power:
+        read += 2 * 128 * 4 * 2 + 4
+        write += 128 * 128 * 4 + 16 * 4 + 2 * 16 * 128 * 2
+    return read + write
+
+
+def bench_refit(steps: int, warmup: int):
+    """Window-boundary refit of B=256 x 32 heads (8192 full windows): the
+    quant-only refit (keep smoothing, fold the 16 records in, requantize) and
+    the rank-4 power-iteration refit, each over 5 rotated slot copies."""
+    import torch
+
+    from gdn_state_codec import codec, native
+    from gdn_state_codec.window import WindowSlot
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(13)
+    states = WINDOW_STATES
+    copies = []
+    for _ in range(ROTATIONS):
+        x = _c1_style_state((states, 128, 128), gen, dev)
+        slot = WindowSlot.allocate(states, dev)
+        codec.encode(x, codec.LAYOUT_VALUE_KEY, slot.residual, slot.smoothing, slot.scales)
+        del x
+        for t in (slot.compensator_keys, slot.compensator_values, slot.record_keys,
+                  slot.record_corrections):
+            t.copy_((torch.randn(t.shape, device=dev, generator=gen) * 0.02).to(torch.float16))
+        slot.record_decay.uniform_(0.93, 0.99, generator=gen)
+        nxt = WindowSlot.allocate(states, dev)
+        copies.append((slot, nxt))
+    workspace = torch.empty((states, 128, 128), dtype=torch.float32, device=dev)
+    lib, stream = native(), torch.cuda.current_stream().cuda_stream
+
+    def refit(r, power):
+        slot, nxt = copies[r]
+        return lib.window_boundary_launch_v1(
+            stream, *slot.pointers(), nxt.residual.data_ptr(), nxt.smoothing.data_ptr(),
+            nxt.scales.data_ptr(), nxt.compensator_keys.data_ptr(),
+            nxt.compensator_values.data_ptr(), workspace.data_ptr(), states, power)
+
+    results = {}
+    for name, power in (("quant_only", 0), ("power", REFIT_POWER_ITERATIONS)):
+        pairs = []
+        for i in range(max(warmup, 1) * ROTATIONS + steps):
+            r = i % ROTATIONS
+            copies[r][0].positions[:, 0] = 16  # a full window (the power refit clears it)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            assert refit(r, power) == 0
+            b.record()
+            if i >= max(warmup, 1) * ROTATIONS:
+                pairs.append((a, b))
+        us = sum(_events_ms(pairs)) / len(pairs) * 1e3
+        assert all(bool((c[0].positions[:, 0] == 0).all()) for c in copies)
+        nbytes = refit_bytes(power > 0) * states
+        results[name] = {"us_per_refit": us, "GBps": nbytes / (us * 1e-6) / 1e9,
+                         "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+                         "bytes_per_refit": nbytes}
+        _log(f"window refit {name}: {us:.1f} us, {results[name]['GBps']:.0f} GB/s")
+    results["workload"] = ("window-boundary refit of B=256 x 32 heads (8192 full windows, "
+                           "[value][key] codes)")
+    results["power_iterations"] = REFIT_POWER_ITERATIONS
+    results["rotated_state_copies"] = ROTATIONS
+    del copies, workspace
+    return results
+
+
 CAPSULE_GEOMETRY = "0123456789abcdef" * 4
 SHA_BLOCKS_PER_CAPSULE = lambda p: (21624 + 1536 * p + 9 + 63) // 64  # noqa: E731
 
@@ -541,6 +621,7 @@ def profile_pass() -> int:
     bench_decode_projection(1, 0)
     bench_chunked_projection(1, 0)
     bench_window_step(0)
+    bench_refit(1, 0)
     bench_capsule(1, 0)
     torch.cuda.synchronize()
     print(json.dumps({"profile_pass": "done"}), flush=True)
@@ -600,6 +681,8 @@ def main() -> int:
             "bytes_per_step": C4_BYTES, "rotated_state_copies": ROTATIONS}
         torch.cuda.empty_cache()
         extra["windowed_step"] = bench_window_step(args.warmup)
+        torch.cuda.empty_cache()
+        extra["window_refit"] = bench_refit(max(args.steps // 2, 5), 1)
         torch.cuda.empty_cache()
         extra["capsule"] = bench_capsule(max(args.steps // 4, 3), args.warmup)
         if not args.no_cpu:
