@@ -16,8 +16,11 @@
 //
 // One workgroup per state; each wavefront owns 32 value columns and each lane
 // two keys, so a column is one coalesced 128-byte row read and write.  The
-// arithmetic keeps the reference's statement order with separately rounded
-// multiplies and adds, making the result bit-identical to its CPU statement.
+// per-column scalars (corr_j[v] * suffix_j and (scale[v] * S) / 127) are formed
+// once per state in LDS, the 32 column maxima come from one reduce-scatter and
+// their multipliers from one vector division.  The arithmetic keeps the
+// reference's statement order with separately rounded multiplies and adds,
+// making the result bit-identical to its CPU statement.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -62,9 +65,44 @@ __device__ __forceinline__ uint32_t rint_through_half(float t) {
   return static_cast<uint32_t>(static_cast<int32_t>(__builtin_rintf(h))) & 0xFFu;
 }
 
+// One halving exchange of a max reduce-scatter over lane bit kMask: the lane
+// with the bit clear keeps v[0, N/2), its partner v[N/2, N), and each takes
+// the max with the partner's copy of the half it keeps.  Recursion (not a
+// runtime loop) keeps every array index a constant, so v stays in registers.
+template <int N, int kMask>
+__device__ __forceinline__ void halve_max(float* v, int lane) {
+  if constexpr (N > 1) {
+    constexpr int n = N / 2;
+    const bool up = (lane & kMask) != 0;
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+      const float lo = v[i];
+      const float hi = v[i + n];
+      const float send = up ? lo : hi;
+      const float keep = up ? hi : lo;
+      v[i] = fmaxf(keep, __shfl_xor(send, kMask));
+    }
+    halve_max<n, kMask / 2>(v, lane);
+  }
+}
+
+// Reduce-scatter of per-lane column maxima: v[c] holds this lane's max for
+// column c (c < 32); afterwards lane L holds the wave-wide max of column
+// L >> 1 (five halvings over lane bits 5..1, one exchange over bit 0; max is
+// exact, so the grouping does not change the result).
+__device__ __forceinline__ float reduce_scatter_max32(float (&v)[32], int lane) {
+  halve_max<32, 32>(v, lane);
+  return fmaxf(v[0], __shfl_xor(v[0], 1));
+}
+
 template <bool kMerged>
 __global__ __launch_bounds__(kThreads) void quant_only_refit_kernel(RefitArgs a) {
-  __shared__ float corrections[kWindow][kDim];
+  // Per-state tables, formed once: corr_j[v] * suffix_j (the record terms'
+  // per-column scalars) and (scale[v] * S) / 127, with the same fp32
+  // roundings as evaluating them per element.
+  __shared__ __align__(16) float scaled_corrections[kDim][kWindow];
+  __shared__ float factors[kDim];
+  __shared__ float multipliers[kWaves][kColumnsPerWave];
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
@@ -80,14 +118,30 @@ __global__ __launch_bounds__(kThreads) void quant_only_refit_kernel(RefitArgs a)
     suffix[j] = boundary_suffix;
     boundary_suffix *= a.record_decay[record_base + j];
   }
+  const int k0 = 2 * lane;
+  const int column0 = wave * kColumnsPerWave;
+  const int8_t* codes = a.residual + state * kTile;
+  // This lane's two codes of each of the wave's 32 columns (rows of [v][k]).
+  uint32_t pair[kColumnsPerWave];
+#pragma unroll
+  for (int c = 0; c < kColumnsPerWave; ++c) {
+    pair[c] = *reinterpret_cast<const uint16_t*>(codes + (column0 + c) * kDim + k0);
+  }
   if constexpr (!kMerged) {
-    for (int i = t; i < kWindow * kDim / 2; i += kThreads) {
-      const uint32_t w = reinterpret_cast<const uint32_t*>(a.record_corrections + record_base * kDim)[i];
-      corrections[(2 * i) / kDim][(2 * i) % kDim] = half_bits_to_float(w & 0xFFFFu);
-      corrections[(2 * i + 1) / kDim][(2 * i + 1) % kDim] = half_bits_to_float(w >> 16);
+    // Threads 0..127 take records 0..7 of column t, threads 128..255 records
+    // 8..15 of column t - 128: coalesced 256-byte fp16 rows per record.
+    const int v = t & (kDim - 1);
+    const int j0 = (t >> 7) * (kWindow / 2);
+#pragma unroll
+    for (int jj = 0; jj < kWindow / 2; ++jj) {
+      const int j = j0 + jj;
+      float sfx = suffix[jj];
+      if (j0 != 0) sfx = suffix[jj + kWindow / 2];
+      scaled_corrections[v][j] =
+          half_bits_to_float(a.record_corrections[(record_base + j) * kDim + v]) * sfx;
     }
   }
-  const int k0 = 2 * lane;
+  if (t < kDim) factors[t] = a.scales[vector_base + t] * boundary_suffix / 127.0f;
   const float2 sm = *reinterpret_cast<const float2*>(a.smoothing + vector_base + k0);
   float key0[kWindow], key1[kWindow];
   if constexpr (!kMerged) {
@@ -100,36 +154,59 @@ __global__ __launch_bounds__(kThreads) void quant_only_refit_kernel(RefitArgs a)
   }
   __syncthreads();
 
-  const int8_t* codes = a.residual + state * kTile;
-  int8_t* out = a.next_residual + state * kTile;
+  // m[k] = w[k] / s[k] for the wave's 32 columns, kept in registers.
+  float m0[kColumnsPerWave], m1[kColumnsPerWave];
+#pragma unroll
   for (int c = 0; c < kColumnsPerWave; ++c) {
-    const int v = wave * kColumnsPerWave + c;
-    const uint32_t pair = *reinterpret_cast<const uint16_t*>(codes + v * kDim + k0);
-    const float factor = a.scales[vector_base + v] * boundary_suffix / 127.0f;
-    float w0 = static_cast<float>(static_cast<int8_t>(pair & 0xFFu)) * factor * sm.x;
-    float w1 = static_cast<float>(static_cast<int8_t>(pair >> 8)) * factor * sm.y;
+    const int v = column0 + c;
+    const float factor = factors[v];
+    float w0 = static_cast<float>(static_cast<int8_t>(pair[c] & 0xFFu)) * factor * sm.x;
+    float w1 = static_cast<float>(static_cast<int8_t>(pair[c] >> 8)) * factor * sm.y;
     if constexpr (kMerged) {
       const float2 merge = *reinterpret_cast<const float2*>(a.record_merge + state * kTile + v * kDim + k0);
       w0 = w0 + merge.x;
       w1 = w1 + merge.y;
     } else {
+      float scalar[kWindow];
+#pragma unroll
+      for (int q = 0; q < kWindow; q += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(&scaled_corrections[v][q]);
+        scalar[q] = x.x;
+        scalar[q + 1] = x.y;
+        scalar[q + 2] = x.z;
+        scalar[q + 3] = x.w;
+      }
 #pragma unroll
       for (int j = 0; j < kWindow; ++j) {
-        const float scalar = corrections[j][v] * suffix[j];
-        w0 = key0[j] * scalar + w0;
-        w1 = key1[j] * scalar + w1;
+        w0 = key0[j] * scalar[j] + w0;
+        w1 = key1[j] * scalar[j] + w1;
       }
     }
-    w0 = w0 / sm.x;
-    w1 = w1 / sm.y;
-    const float maximum = wave_max(fmaxf(fabsf(w0), fabsf(w1)));
-    if (lane == 0) a.next_scales[vector_base + v] = maximum;
-    const float multiplier = maximum > 0.0f ? 127.0f / maximum : 0.0f;
-    float t0 = w0 * multiplier, t1 = w1 * multiplier;
+    m0[c] = w0 / sm.x;
+    m1[c] = w1 / sm.y;
+  }
+
+  // Column maxima (scale'), then every column's multiplier 127 / scale' in one
+  // vector division: lane 2c holds column c.
+  float column_max[kColumnsPerWave];
+#pragma unroll
+  for (int c = 0; c < kColumnsPerWave; ++c) column_max[c] = fmaxf(fabsf(m0[c]), fabsf(m1[c]));
+  const float maximum = reduce_scatter_max32(column_max, lane);
+  if ((lane & 1) == 0) {
+    a.next_scales[vector_base + column0 + (lane >> 1)] = maximum;
+    multipliers[wave][lane >> 1] = maximum > 0.0f ? 127.0f / maximum : 0.0f;
+  }
+  wave_lds_sync();
+
+  int8_t* out = a.next_residual + state * kTile;
+#pragma unroll
+  for (int c = 0; c < kColumnsPerWave; ++c) {
+    const float multiplier = multipliers[wave][c];
+    float t0 = m0[c] * multiplier, t1 = m1[c] * multiplier;
     t0 = fminf(fmaxf(t0, -127.0f), 127.0f);
     t1 = fminf(fmaxf(t1, -127.0f), 127.0f);
     const uint32_t packed = rint_through_half(t0) | (rint_through_half(t1) << 8);
-    *reinterpret_cast<uint16_t*>(out + v * kDim + k0) = static_cast<uint16_t>(packed);
+    *reinterpret_cast<uint16_t*>(out + (column0 + c) * kDim + k0) = static_cast<uint16_t>(packed);
   }
   // Smoothing kept, compensators zero, position reset (the finalize kernel).
   if (t < kDim) a.next_smoothing[vector_base + t] = a.smoothing[vector_base + t];
