@@ -191,19 +191,37 @@ struct FinishShared {
   float read[kDim];
   float query[kDim];
   float write[kDim];
-  float basis[kRank + kWindow][kDim];
+  union {
+    // Compensator then record keys as fp16 bits (exact; widened when read).
+    uint16_t basis[kRank + kWindow][kDim];
+    // Fused kernel only: the projections by value, read back before the keys
+    // are staged (a wavefront's LDS accesses complete in program order).
+    int32_t projected[kDim][4];
+  };
   float sums[1 + 2 * kRank + 2 * kWindow];
 };
 
-// Finishes one state at position p < 16 for the two values value_of[0..1] of
-// this lane, given the int32 projections P[e][c] (c = hi0, lo0, hi1, lo1) and
-// the dynamic scales.
+// Finishes one state at position p < 16 for this lane's two values
+// 2*lane, 2*lane+1, given the int32 projections P[e][c] (c = hi0, lo0, hi1,
+// lo1) and the dynamic scales.  The per-value operands (scales, compensator
+// values, values and the p record corrections) are loaded first, so they are
+// in flight during the key staging and the sequential sums.
 __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& sh,
                              const StepVectors& v, uint32_t state, uint32_t p,
-                             int lane, const int (&value_of)[2],
-                             const int32_t (&P)[2][4], const float (&ds)[4]) {
+                             int lane, const int32_t (&P)[2][4], const float (&ds)[4]) {
   const uint64_t vector_base = static_cast<uint64_t>(state) * kDim;
   const uint64_t record_base = static_cast<uint64_t>(state) * kWindow;
+  const int column0 = 2 * lane;
+  const float2 scale = *reinterpret_cast<const float2*>(a.scales + vector_base + column0);
+  const uint4 cv = *reinterpret_cast<const uint4*>(a.comp_values + (vector_base + column0) * kRank);
+  const uint32_t value_word = *reinterpret_cast<const uint32_t*>(a.values + vector_base + column0);
+  uint32_t correction_word[kWindow];
+#pragma unroll
+  for (int j = 0; j < kWindow; ++j) {
+    correction_word[j] = j < static_cast<int>(p)
+        ? *reinterpret_cast<const uint32_t*>(a.record_corrections + (record_base + j) * kDim + column0)
+        : 0u;
+  }
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     sh.read[2 * lane + e] = v.read[e];
@@ -216,17 +234,15 @@ __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& 
     const uint32_t words[4] = {ck.x, ck.y, ck.z, ck.w};
 #pragma unroll
     for (int r = 0; r < kRank; ++r) {
-      sh.basis[r][2 * lane] = half_bits_to_float((words[r >> 1] >> (16 * (r & 1))) & 0xFFFFu);
-      sh.basis[r][2 * lane + 1] =
-          half_bits_to_float((words[2 + (r >> 1)] >> (16 * (r & 1))) & 0xFFFFu);
+      const uint32_t k0 = (words[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
+      const uint32_t k1 = (words[2 + (r >> 1)] >> (16 * (r & 1))) & 0xFFFFu;
+      *reinterpret_cast<uint32_t*>(&sh.basis[r][2 * lane]) = k0 | (k1 << 16);
     }
 #pragma unroll
     for (int j = 0; j < kWindow; ++j) {
       if (j < static_cast<int>(p)) {
-        const uint32_t rk = *reinterpret_cast<const uint32_t*>(
-            a.record_keys + (record_base + j) * kDim + 2 * lane);
-        sh.basis[kRank + j][2 * lane] = half_bits_to_float(rk & 0xFFFFu);
-        sh.basis[kRank + j][2 * lane + 1] = half_bits_to_float(rk >> 16);
+        *reinterpret_cast<uint32_t*>(&sh.basis[kRank + j][2 * lane]) =
+            *reinterpret_cast<const uint32_t*>(a.record_keys + (record_base + j) * kDim + 2 * lane);
       }
     }
   }
@@ -237,11 +253,11 @@ __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& 
   // acc += basis * x (read side) or acc += basis * query * gate (output side).
   const int sums = 1 + 2 * kRank + 2 * static_cast<int>(p);
   if (lane < sums) {
-    const float* basis;
+    const uint16_t* basis;
     const float* x;
     bool gated;
     if (lane == 0) {
-      basis = sh.write;
+      basis = nullptr;  // the update sum w . q reads sh.write
       x = sh.query;
       gated = false;
     } else if (lane <= 2 * kRank) {
@@ -255,12 +271,15 @@ __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& 
       x = gated ? sh.query : sh.read;
     }
     float acc = 0.0f;
-    if (gated) {
+    if (lane == 0) {
 #pragma unroll 16
-      for (int row = 0; row < kDim; ++row) acc += basis[row] * x[row] * v.gate;
+      for (int row = 0; row < kDim; ++row) acc += sh.write[row] * x[row];
+    } else if (gated) {
+#pragma unroll 16
+      for (int row = 0; row < kDim; ++row) acc += half_bits_to_float(basis[row]) * x[row] * v.gate;
     } else {
 #pragma unroll 16
-      for (int row = 0; row < kDim; ++row) acc += basis[row] * x[row];
+      for (int row = 0; row < kDim; ++row) acc += half_bits_to_float(basis[row]) * x[row];
     }
     sh.sums[lane] = acc;
   }
@@ -273,38 +292,50 @@ __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& 
     suffix[j] = boundary_suffix;
     if (j < static_cast<int>(p)) boundary_suffix *= a.record_decay[record_base + j];
   }
-  uint16_t* correction_out = a.record_corrections + (record_base + p) * kDim;
+  const float value_scale[2] = {scale.x, scale.y};
+  const uint32_t comp_words[4] = {cv.x, cv.y, cv.z, cv.w};
+  uint32_t output_bits = 0, correction_bits = 0;
+  float output_f32[2];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const int column = value_of[e];
-    const float scale = a.scales[vector_base + column];
     float state_read = (static_cast<float>(P[e][0]) * ds[0] +
-                        static_cast<float>(P[e][1]) * ds[2]) / 127.0f * scale * boundary_suffix;
+                        static_cast<float>(P[e][1]) * ds[2]) / 127.0f * value_scale[e] *
+                       boundary_suffix;
     float output_read = (static_cast<float>(P[e][2]) * ds[1] +
-                         static_cast<float>(P[e][3]) * ds[3]) / 127.0f * scale * boundary_suffix;
-    const uint2 cv = *reinterpret_cast<const uint2*>(a.comp_values + (vector_base + column) * kRank);
+                         static_cast<float>(P[e][3]) * ds[3]) / 127.0f * value_scale[e] *
+                        boundary_suffix;
 #pragma unroll
     for (int r = 0; r < kRank; ++r) {
-      const float b = half_bits_to_float(((r < 2 ? cv.x : cv.y) >> (16 * (r & 1))) & 0xFFFFu);
+      const float b = half_bits_to_float((comp_words[2 * e + (r >> 1)] >> (16 * (r & 1))) & 0xFFFFu);
       state_read += b * sh.sums[1 + r] * boundary_suffix;
       output_read += b * sh.sums[1 + kRank + r] * boundary_suffix;
     }
-    for (int j = 0; j < static_cast<int>(p); ++j) {
-      const float b = half_bits_to_float(a.record_corrections[(record_base + j) * kDim + column]);
-      state_read += b * sh.sums[1 + 2 * kRank + j] * suffix[j];
-      output_read += b * sh.sums[1 + 2 * kRank + p + j] * suffix[j];
+#pragma unroll
+    for (int j = 0; j < kWindow; ++j) {
+      if (j < static_cast<int>(p)) {
+        const float b = half_bits_to_float((correction_word[j] >> (16 * e)) & 0xFFFFu);
+        state_read += b * sh.sums[1 + 2 * kRank + j] * suffix[j];
+        output_read += b * sh.sums[1 + 2 * kRank + p + j] * suffix[j];
+      }
     }
-    const float value = a.bf16 ? bf16_to_float(a.values[vector_base + column])
-                               : half_bits_to_float(a.values[vector_base + column]);
+    const uint32_t value_bits = (value_word >> (16 * e)) & 0xFFFFu;
+    const float value = a.bf16 ? bf16_to_float(static_cast<uint16_t>(value_bits))
+                               : half_bits_to_float(value_bits);
     const float correction = value - state_read;
     const float out = output_read + correction * update;
-    if (a.bf16) {
-      static_cast<uint16_t*>(a.outputs)[vector_base + column] = float_to_bf16(out);
-    } else {
-      static_cast<float*>(a.outputs)[vector_base + column] = out;
-    }
-    correction_out[column] = static_cast<uint16_t>(float_to_half_bits(correction));
+    output_f32[e] = out;
+    output_bits |= static_cast<uint32_t>(float_to_bf16(out)) << (16 * e);
+    correction_bits |= float_to_half_bits(correction) << (16 * e);
   }
+  if (a.bf16) {
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.outputs) + vector_base + column0) =
+        output_bits;
+  } else {
+    *reinterpret_cast<float2*>(static_cast<float*>(a.outputs) + vector_base + column0) =
+        make_float2(output_f32[0], output_f32[1]);
+  }
+  *reinterpret_cast<uint32_t*>(a.record_corrections + (record_base + p) * kDim + column0) =
+      correction_bits;
   *reinterpret_cast<uint32_t*>(a.record_keys + (record_base + p) * kDim + 2 * lane) =
       v.record_key_bits;
   if (lane == 0) {
@@ -447,17 +478,16 @@ __global__ __launch_bounds__(kThreads) void finish_pair_kernel(
   const uint32_t p = fa.positions[static_cast<uint64_t>(state) * kPositionStride];
   if (p >= kWindow) return;
   const StepVectors v = load_vectors(in, state, lane);
-  const int value_of[2] = {2 * lane, 2 * lane + 1};
   int32_t P[2][4];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const int4 w = *reinterpret_cast<const int4*>(
-        projected + (static_cast<uint64_t>(state) * kDim + value_of[e]) * kPairColumns);
+        projected + (static_cast<uint64_t>(state) * kDim + 2 * lane + e) * kPairColumns);
     P[e][0] = w.x; P[e][1] = w.y; P[e][2] = w.z; P[e][3] = w.w;
   }
   const float4 d = *reinterpret_cast<const float4*>(dynamic_scale + static_cast<uint64_t>(state) * kPositionStride);
   const float ds[4] = {d.x, d.y, d.z, d.w};
-  finish_state(fa, shared[wave], v, state, p, lane, value_of, P, ds);
+  finish_state(fa, shared[wave], v, state, p, lane, P, ds);
 }
 
 // Integer analogue of the decode projection's pairwise lane reduction.
@@ -555,16 +585,20 @@ __global__ __launch_bounds__(kThreads) void fused_decode_pair_kernel(
   }
 #pragma unroll
   for (int c = 0; c < 4; ++c) reduce16_over_8_lanes_int(acc[c], lane);
-  const int value_of[2] = {r8 + 8 * (2 * kq), r8 + 8 * (2 * kq + 1)};
+  // Lane holds values r8 + 8 * (2 * kq + e); the finish wants 2 * lane + e.
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    *reinterpret_cast<int4*>(&shared[wave].projected[r8 + 8 * (2 * kq + e)][0]) =
+        make_int4(acc[0][e], acc[1][e], acc[2][e], acc[3][e]);
+  }
+  wave_lds_sync();
   int32_t P[2][4];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) P[e][c] = acc[c][e];
+    const int4 w = *reinterpret_cast<const int4*>(&shared[wave].projected[2 * lane + e][0]);
+    P[e][0] = w.x; P[e][1] = w.y; P[e][2] = w.z; P[e][3] = w.w;
   }
-  // The record key this lane stores covers rows 2*lane..+1 regardless of the
-  // value mapping, as in finish_state.
-  finish_state(fa, shared[wave], v, state, p, lane, value_of, P, ds);
+  finish_state(fa, shared[wave], v, state, p, lane, P, ds);
 }
 
 }  // namespace
