@@ -73,6 +73,13 @@ __device__ __forceinline__ float newton_sqrt(float value) {
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return half_bits_to_float(h); }
+
+// code / 127 for an int8 code: IEEE division by 127 through its correctly
+// rounded reciprocal (div_by_reciprocal is exact for every numerator in
+// [2^-100, 2^120] and for +0, which covers the integers -127..127).
+__device__ __forceinline__ float code_over_127(int8_t code) {
+  return div_by_reciprocal(static_cast<float>(code), kQuantizedMaximum, kInvQuantizedMaximum);
+}
 __device__ __forceinline__ float round_half(float x) {
   return half_bits_to_float(float_to_half_bits(x));
 }
@@ -124,8 +131,8 @@ __device__ void apply_right(PowerShared& sh, const float* vector, float* output,
   float value = 0.0f;
   const float s = sh.smoothing[row];
   for (int column = 0; column < kDim; ++column) {
-    value += static_cast<float>(sh.code[column * kCodeStride + row]) / 127.0f * s *
-             sh.scales[column] * vector[column] * bs;
+    value += code_over_127(sh.code[column * kCodeStride + row]) * s * sh.scales[column] *
+             vector[column] * bs;
   }
   for (int r = 0; r < kRank; ++r) value += sh.ck[row * kRank + r] * sh.old_projection[r] * bs;
   for (int j = 0; j < kWindow; ++j) {
@@ -146,8 +153,7 @@ __device__ void apply_transpose(PowerShared& sh, const float* vector, float* out
   const float scale = sh.scales[column];
   const int8_t* code = sh.code + column * kCodeStride;
   for (int row = 0; row < kDim; ++row) {
-    value += static_cast<float>(code[row]) / 127.0f * sh.smoothing[row] * scale *
-             vector[row] * bs;
+    value += code_over_127(code[row]) * sh.smoothing[row] * scale * vector[row] * bs;
   }
   for (int r = 0; r < kRank; ++r) value += sh.cv[column * kRank + r] * sh.old_projection[r] * bs;
   for (int j = 0; j < kWindow; ++j) {
@@ -162,8 +168,8 @@ __device__ void apply_transpose(PowerShared& sh, const float* vector, float* out
 // ResidualCell (:223-251).
 __device__ __forceinline__ float residual_cell(const PowerShared& sh, int row, int column,
                                                float bs) {
-  float value = static_cast<float>(sh.code[column * kCodeStride + row]) / 127.0f *
-                sh.smoothing[row] * sh.scales[column] * bs;
+  float value = code_over_127(sh.code[column * kCodeStride + row]) * sh.smoothing[row] *
+                sh.scales[column] * bs;
   for (int r = 0; r < kRank; ++r) {
     value += sh.ck[row * kRank + r] * sh.cv[column * kRank + r] * bs;
     value -= sh.nk[row * kRank + r] * sh.nv[column * kRank + r];
