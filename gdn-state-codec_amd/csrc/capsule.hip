@@ -53,7 +53,8 @@ static_assert(content_bytes(0) + kDigestChars == 21688, "capsule size");
 static_assert(content_bytes(0) % 64 == 56, "the digest tail spans two blocks");
 
 constexpr int kThreads = 256;
-constexpr int kDigestLanes = 64;
+constexpr int kDigestLanes = 64;                 // capsules per digest workgroup
+constexpr int kDigestThreads = 2 * kDigestLanes;  // producer + consumer wavefront
 
 // The expected / written identity, as kernel-argument words.
 struct Identity {
@@ -100,102 +101,61 @@ __device__ __forceinline__ uint32_t majority(uint32_t x, uint32_t y, uint32_t z)
   return __builtin_amdgcn_bitop3_b32(x, y, z, 0xE8);  // (x&y) ^ (x&z) ^ (y&z)
 }
 
-// One compression (section 6.2.2); w holds the block's 16 words and is
-// overwritten by the message schedule.
-__device__ __forceinline__ void compress(uint32_t h[8], uint32_t w[16]) {
-  uint32_t a = h[0], b = h[1], c = h[2], d = h[3], e = h[4], f = h[5], g = h[6], k = h[7];
-#pragma unroll
-  for (int t = 0; t < 64; ++t) {
-    uint32_t wt;
-    if (t < 16) {
-      wt = w[t];
-    } else {
-      const uint32_t w15 = w[(t - 15) & 15];
-      const uint32_t w2 = w[(t - 2) & 15];
-      const uint32_t s0 = xor3(rotr(w15, 7), rotr(w15, 18), w15 >> 3);
-      const uint32_t s1 = xor3(rotr(w2, 17), rotr(w2, 19), w2 >> 10);
-      wt = w[t & 15] + s0 + w[(t - 7) & 15] + s1;
-      w[t & 15] = wt;
-    }
-    const uint32_t t1 =
-        k + xor3(rotr(e, 6), rotr(e, 11), rotr(e, 25)) + choose(e, f, g) + kRound[t] + wt;
-    const uint32_t t2 = xor3(rotr(a, 2), rotr(a, 13), rotr(a, 22)) + majority(a, b, c);
-    k = g;
-    g = f;
-    f = e;
-    e = d + t1;
-    d = c;
-    c = b;
-    b = a;
-    a = t1 + t2;
-  }
-  h[0] += a;
-  h[1] += b;
-  h[2] += c;
-  h[3] += d;
-  h[4] += e;
-  h[5] += f;
-  h[6] += g;
-  h[7] += k;
-}
-
-// SHA-256 of content[0, size) as 16 words of lowercase hex characters (the
-// reference's Sha256Hex string, 4 characters per little-endian word).
-// content is 8-byte aligned; the tail may read up to 3 bytes past `size`,
-// which the caller guarantees lie inside the capsule (the digest follows).
-__device__ void sha256_hex(const uint8_t* content, uint32_t size, uint32_t hex[16]) {
-  uint32_t h[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) h[i] = kInitial[i];
-  const uint32_t blocks = size / 64;
-  const uint64_t* src = reinterpret_cast<const uint64_t*>(content);
-  uint64_t next[8];
-  if (blocks > 0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) next[i] = src[i];
-  }
-  for (uint32_t block = 0; block < blocks; ++block) {
-    uint32_t w[16];
+// Block `block` of the padded message of content[0, size) (FIPS 180-4
+// section 5.1.1: the bytes, 0x80, zeros, the 64-bit big-endian bit length) as
+// 16 big-endian words.  Full blocks come from `full_words` (the caller's
+// prefetched loads); the tail reads aligned words and may read up to 3 bytes
+// past `size`, which the caller guarantees lie inside the capsule (the digest
+// follows the content).
+__device__ __forceinline__ void message_block(const uint8_t* content, uint32_t size,
+                                              uint32_t block, const uint64_t (&full_words)[8],
+                                              uint32_t (&w)[16]) {
+  const uint32_t full = size / 64;
+  if (block < full) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      w[2 * i] = big_endian(static_cast<uint32_t>(next[i]));
-      w[2 * i + 1] = big_endian(static_cast<uint32_t>(next[i] >> 32));
+      w[2 * i] = big_endian(static_cast<uint32_t>(full_words[i]));
+      w[2 * i + 1] = big_endian(static_cast<uint32_t>(full_words[i] >> 32));
     }
-    // Issue the next block's loads before this block's compression.
-    if (block + 1 < blocks) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) next[i] = src[8 * (block + 1) + i];
-    }
-    compress(h, w);
+    return;
   }
-  // Padding (section 5.1.1): 0x80, zeros, the 64-bit big-endian bit length.
-  const uint32_t rest = size - 64 * blocks;
-  const uint32_t* tail = reinterpret_cast<const uint32_t*>(content + 64 * blocks);
-  uint32_t w[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint32_t start = 4u * i;
-    uint32_t word = 0;
-    if (start + 4 <= rest) {
-      word = big_endian(tail[i]);
-    } else if (start < rest) {
-      const uint32_t keep = rest - start;  // 1..3 message bytes in this word
-      word = (big_endian(tail[i]) & (0xFFFFFFFFu << (8 * (4 - keep)))) |
-             (0x80u << (8 * (3 - keep)));
-    } else if (start == rest) {
-      word = 0x80000000u;
-    }
-    w[i] = word;
-  }
+  const uint32_t rest = size - 64 * full;
   const uint64_t bits = static_cast<uint64_t>(size) * 8u;
-  if (rest > 55) {
-    compress(h, w);
+  if (block == full) {
+    const uint32_t* tail = reinterpret_cast<const uint32_t*>(content + 64 * full);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t start = 4u * i;
+      uint32_t word = 0;
+      if (start + 4 <= rest) {
+        word = big_endian(tail[i]);
+      } else if (start < rest) {
+        const uint32_t keep = rest - start;  // 1..3 message bytes in this word
+        word = (big_endian(tail[i]) & (0xFFFFFFFFu << (8 * (4 - keep)))) |
+               (0x80u << (8 * (3 - keep)));
+      } else if (start == rest) {
+        word = 0x80000000u;
+      }
+      w[i] = word;
+    }
+    if (rest <= 55) {
+      w[14] = static_cast<uint32_t>(bits >> 32);
+      w[15] = static_cast<uint32_t>(bits);
+    }
+  } else {  // the length block after a tail of more than 55 bytes
 #pragma unroll
     for (int i = 0; i < 14; ++i) w[i] = 0;
+    w[14] = static_cast<uint32_t>(bits >> 32);
+    w[15] = static_cast<uint32_t>(bits);
   }
-  w[14] = static_cast<uint32_t>(bits >> 32);
-  w[15] = static_cast<uint32_t>(bits);
-  compress(h, w);
+}
+
+// Compression blocks of the padded message of `size` bytes.
+__device__ __forceinline__ uint32_t message_blocks(uint32_t size) { return (size + 9 + 63) / 64; }
+
+// 16 words of lowercase hex characters of the digest (the reference's
+// Sha256Hex string, 4 characters per little-endian word).
+__device__ __forceinline__ void digest_hex(const uint32_t (&h)[8], uint32_t (&hex)[16]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     uint32_t chars[2] = {0, 0};
@@ -219,51 +179,172 @@ struct DigestArgs {
   uint32_t states;
 };
 
+// One workgroup hashes 64 capsules, one per lane, with two wavefronts: the
+// producer loads each 64-byte block, expands the message schedule and writes
+// K[t] + W[t] for the block's 64 rounds to a double-buffered LDS ring; the
+// consumer runs only the round function from the ring (section 6.2.2), so
+// the serial chain of each capsule carries about two thirds of the
+// instructions of a full compression.  One barrier per block: the producer
+// fills slot b + 1 while the consumer works on slot b, and a slot is
+// refilled only after the barrier the consumer reaches when done with it.
+//
 // kVerify = false: write the digest of each serialized capsule (lengths[i] = 0
 // marks a state the pack kernel skipped).  kVerify = true: the first checks of
 // Restore (state_capsule.cpp:481-494), status[i] = 0 when they all pass.
 template <bool kVerify>
-__global__ __launch_bounds__(kDigestLanes) void capsule_digest_kernel(DigestArgs a) {
-  const uint32_t s = blockIdx.x * kDigestLanes + threadIdx.x;
-  if (s >= a.states) return;
-  const uint64_t offset = a.offsets[s];
-  const uint32_t length = a.lengths[s];
-  if constexpr (kVerify) {
-    if ((offset & 7u) != 0 || offset > a.capacity || length > a.capacity - offset) {
-      a.status[s] = GDN_STATE_CODEC_CAPSULE_EXTENT;
-      return;
-    }
-    if (length < kMinimumCapsule) {
-      a.status[s] = GDN_STATE_CODEC_CAPSULE_TRUNCATED;
-      return;
-    }
-  } else {
-    if (length == 0) return;
-  }
-  uint8_t* base = a.capsules + offset;
-  const uint32_t content = length - kDigestChars;
+__global__ __launch_bounds__(kDigestThreads) void capsule_digest_kernel(DigestArgs a) {
+  __shared__ __align__(16) uint4 ring[2][16][kDigestLanes];  // [slot][round / 4][lane]
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const uint32_t s = blockIdx.x * kDigestLanes + lane;
+
+  // Per-capsule checks, evaluated identically by both wavefronts so that
+  // their block counts (and so their barrier counts) agree.
+  uint32_t status = GDN_STATE_CODEC_CAPSULE_OK;
+  bool hash = false;
+  uint8_t* base = nullptr;
+  uint32_t content = 0;
   uint32_t recorded[16];
-  if constexpr (kVerify) {
-    if (*reinterpret_cast<const uint64_t*>(base) != kMagicWord) {
-      a.status[s] = GDN_STATE_CODEC_CAPSULE_MAGIC;
-      return;
-    }
-    bool lowercase_hex = true;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) recorded[i] = 0;
+  for (int i = 0; i < 16; ++i) recorded[i] = 0;
+  if (s < a.states) {
+    const uint64_t offset = a.offsets[s];
+    const uint32_t length = a.lengths[s];
+    hash = true;
+    if constexpr (kVerify) {
+      if ((offset & 7u) != 0 || offset > a.capacity || length > a.capacity - offset) {
+        status = GDN_STATE_CODEC_CAPSULE_EXTENT;
+        hash = false;
+      } else if (length < kMinimumCapsule) {
+        status = GDN_STATE_CODEC_CAPSULE_TRUNCATED;
+        hash = false;
+      }
+    } else {
+      hash = length != 0;
+    }
+    if (hash) {
+      base = a.capsules + offset;
+      content = length - kDigestChars;
+      if constexpr (kVerify) {
+        if (*reinterpret_cast<const uint64_t*>(base) != kMagicWord) {
+          status = GDN_STATE_CODEC_CAPSULE_MAGIC;
+          hash = false;
+        } else {
+          bool lowercase_hex = true;
 #pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      const uint32_t ch = base[content + i];
-      lowercase_hex = lowercase_hex && (ch - '0' < 10u || ch - 'a' < 6u);
-      recorded[i >> 2] |= ch << (8 * (i & 3));
+          for (int i = 0; i < 64; ++i) {
+            const uint32_t ch = base[content + i];
+            lowercase_hex = lowercase_hex && (ch - '0' < 10u || ch - 'a' < 6u);
+            recorded[i >> 2] |= ch << (8 * (i & 3));
+          }
+          if (!lowercase_hex) {
+            status = GDN_STATE_CODEC_CAPSULE_DIGEST_ENCODING;
+            hash = false;
+          }
+        }
+      }
     }
-    if (!lowercase_hex) {
-      a.status[s] = GDN_STATE_CODEC_CAPSULE_DIGEST_ENCODING;
-      return;
+  }
+  const uint32_t blocks = hash ? message_blocks(content) : 0u;
+  uint32_t wave_blocks = blocks;
+#pragma unroll
+  for (int mask = 32; mask >= 1; mask >>= 1) {
+    const uint32_t other = __shfl_xor(wave_blocks, mask);
+    wave_blocks = other > wave_blocks ? other : wave_blocks;
+  }
+
+  if (wave == 0) {
+    // ---- producer: message schedule plus round constants ----
+    const uint32_t full = content / 64;
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(base);
+    uint64_t next[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) next[i] = 0;
+    if (full > 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) next[i] = src[i];
     }
+    for (uint32_t block = 0; block < wave_blocks; ++block) {
+      if (block < blocks) {
+        uint32_t w[16];
+        message_block(base, content, block, next, w);
+        // Issue the next block's loads before this block's schedule.
+        if (block + 1 < full) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) next[i] = src[8 * (block + 1) + i];
+        }
+        uint4* slot = &ring[block & 1][0][0];
+        uint32_t group[4];
+#pragma unroll
+        for (int t = 0; t < 64; ++t) {
+          uint32_t wt;
+          if (t < 16) {
+            wt = w[t];
+          } else {
+            const uint32_t w15 = w[(t - 15) & 15];
+            const uint32_t w2 = w[(t - 2) & 15];
+            const uint32_t s0 = xor3(rotr(w15, 7), rotr(w15, 18), w15 >> 3);
+            const uint32_t s1 = xor3(rotr(w2, 17), rotr(w2, 19), w2 >> 10);
+            wt = w[t & 15] + s0 + w[(t - 7) & 15] + s1;
+            w[t & 15] = wt;
+          }
+          group[t & 3] = kRound[t] + wt;
+          if ((t & 3) == 3) {
+            slot[(t >> 2) * kDigestLanes + lane] = make_uint4(group[0], group[1], group[2], group[3]);
+          }
+        }
+      }
+      __syncthreads();  // slot (block & 1) is ready
+    }
+    return;
+  }
+
+  // ---- consumer: the round chain ----
+  uint32_t h[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = kInitial[i];
+  for (uint32_t block = 0; block < wave_blocks; ++block) {
+    __syncthreads();  // slot (block & 1) is ready
+    if (block < blocks) {
+      const uint4* slot = &ring[block & 1][0][0];
+      uint32_t va = h[0], vb = h[1], vc = h[2], vd = h[3], ve = h[4], vf = h[5], vg = h[6],
+               vh = h[7];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const uint4 kw4 = slot[q * kDigestLanes + lane];
+        const uint32_t kw[4] = {kw4.x, kw4.y, kw4.z, kw4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t t1 = vh + xor3(rotr(ve, 6), rotr(ve, 11), rotr(ve, 25)) +
+                              choose(ve, vf, vg) + kw[i];
+          const uint32_t t2 = xor3(rotr(va, 2), rotr(va, 13), rotr(va, 22)) + majority(va, vb, vc);
+          vh = vg;
+          vg = vf;
+          vf = ve;
+          ve = vd + t1;
+          vd = vc;
+          vc = vb;
+          vb = va;
+          va = t1 + t2;
+        }
+      }
+      h[0] += va;
+      h[1] += vb;
+      h[2] += vc;
+      h[3] += vd;
+      h[4] += ve;
+      h[5] += vf;
+      h[6] += vg;
+      h[7] += vh;
+    }
+  }
+  if (s >= a.states) return;
+  if (!hash) {
+    if constexpr (kVerify) a.status[s] = status;
+    return;
   }
   uint32_t hex[16];
-  sha256_hex(base, content, hex);
+  digest_hex(h, hex);
   if constexpr (kVerify) {
     bool same = true;
 #pragma unroll
@@ -747,7 +828,7 @@ extern "C" int32_t statecentric_gdn_state_codec_capsule_serialize_launch_v1(
   if (status != gdn::kStatusOk) return status;
   const gdn::DigestArgs digest{capsules, offsets, lengths, capacity, nullptr, states};
   return gdn::launch(gdn::capsule_digest_kernel<false>, dim3(gdn::digest_blocks(states)),
-                     dim3(gdn::kDigestLanes), stream, digest);
+                     dim3(gdn::kDigestThreads), stream, digest);
 }
 
 extern "C" int32_t statecentric_gdn_state_codec_capsule_restore_launch_v1(
@@ -769,7 +850,7 @@ extern "C" int32_t statecentric_gdn_state_codec_capsule_restore_launch_v1(
   const gdn::DigestArgs digest{const_cast<uint8_t*>(capsules), offsets, lengths, capacity,
                                status, states};
   int32_t result = gdn::launch(gdn::capsule_digest_kernel<true>,
-                               dim3(gdn::digest_blocks(states)), dim3(gdn::kDigestLanes),
+                               dim3(gdn::digest_blocks(states)), dim3(gdn::kDigestThreads),
                                stream, digest);
   if (result != gdn::kStatusOk) return result;
   args.capsules = capsules;
