@@ -524,44 +524,130 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
   __shared__ uint32_t header[kHeaderWords];
   __shared__ float sm[kDim], sc[kDim], ck[kDim * kRank], cv[kDim * kRank];
   __shared__ float rec[(kWindow - 1) * kRecordFloats];  // records 0..14
-  __shared__ float maxima[4 + 3 * (kWindow - 1)];
+  // |max| of smoothing, scales, ck, cv, then (decay, key, correction) of each
+  // record, as float bits (non-negative floats order like their bits).
+  __shared__ uint32_t maxima[4 + 3 * (kWindow - 1)];
+  // flags[0]: bit 0 a code equals -128, bit 1 the boundary payload is invalid;
+  // flags[1]: bit j record j holds a non-finite value.
+  __shared__ uint32_t flags[2];
   __shared__ __align__(16) uint8_t tile[kDim * kTileStride];
   const uint32_t s = blockIdx.x;
   const int t = threadIdx.x;
   if (a.status[s] != GDN_STATE_CODEC_CAPSULE_OK) return;  // the digest kernel refused it
   const uint8_t* base = a.capsules + a.offsets[s];
   const uint32_t content = a.lengths[s] - kDigestChars;
-  // Every value below is uniform over the workgroup; checks run in the order
-  // of state_capsule.cpp:497-576 and the first failure names the outcome.
+  if (t < 2) flags[t] = 0u;
+  if (t < 4 + 3 * (kWindow - 1)) maxima[t] = 0u;
+  __syncthreads();
+
+  // Every load the checks need, issued together.  What is present depends
+  // only on the content length; which of it counts is decided below.
+  const bool has_header = content >= kResidualOffset;
+  const bool has_codes = content >= kSmoothingOffset;
+  const bool has_payload = content >= kRecordsOffset;
+  const uint32_t whole = has_payload ? (content - kRecordsOffset) / kRecordBytes : 0u;
+  const uint32_t loaded = whole < kWindow - 1 ? whole : kWindow - 1;
+  if (has_header && t < static_cast<int>(kHeaderWords)) {
+    header[t] = reinterpret_cast<const uint32_t*>(base)[t];
+  }
+  uint64_t codes[8];
+  bool minus128 = false;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) codes[i] = 0;
+  if (has_codes) {
+    const uint64_t* code_words = reinterpret_cast<const uint64_t*>(base + kResidualOffset);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      codes[i] = code_words[i * kThreads + t];
+      minus128 = minus128 || has_byte_0x80(codes[i]);
+    }
+  }
+  float2 key_pair = make_float2(0.0f, 0.0f), value_pair = make_float2(0.0f, 0.0f);
+  bool payload_bad = false;
+  const int lane = t & 63;
+  // A wavefront's 64 values of one slot are reduced first, then merged into
+  // the workgroup's slot by one atomic.
+  const auto merge_max = [&](int slot, float magnitude) {
+    const float m = wave_max(magnitude);
+    if (lane == 0) atomicMax(&maxima[slot], __float_as_uint(m));
+  };
+  if (has_payload) {
+    const float value = *reinterpret_cast<const float*>(base + kSmoothingOffset + 4 * t);
+    if (t < kDim) {
+      sm[t] = value;
+      payload_bad = !(isfinite(value) && value > 0.0f);
+    } else {
+      sc[t - kDim] = value;
+      payload_bad = !(isfinite(value) && value >= 0.0f);
+    }
+    merge_max(t < kDim ? 0 : 1, fabsf(value));  // waves 0-1 smoothing, 2-3 scales
+    key_pair = reinterpret_cast<const float2*>(base + kCompKeysOffset)[t];
+    value_pair = reinterpret_cast<const float2*>(base + kCompValuesOffset)[t];
+    ck[2 * t] = key_pair.x;
+    ck[2 * t + 1] = key_pair.y;
+    cv[2 * t] = value_pair.x;
+    cv[2 * t + 1] = value_pair.y;
+    payload_bad = payload_bad || !isfinite(key_pair.x) || !isfinite(key_pair.y) ||
+                  !isfinite(value_pair.x) || !isfinite(value_pair.y);
+    merge_max(2, fmaxf(fabsf(key_pair.x), fabsf(key_pair.y)));
+    merge_max(3, fmaxf(fabsf(value_pair.x), fabsf(value_pair.y)));
+    // w = i * 256 + t: a wavefront's 64 values lie in one 128-value vector.
+    const float* src = reinterpret_cast<const float*>(base + kRecordsOffset);
+    for (uint32_t w = t; w < kRecordFloats * loaded; w += kThreads) {
+      const float value = src[w];
+      rec[w] = value;
+      const uint32_t j = w / kRecordFloats;
+      if (!isfinite(value)) atomicOr(&flags[1], 1u << j);
+      merge_max(4 + static_cast<int>(w / kDim), fabsf(value));
+    }
+  }
+  if (minus128 || payload_bad) {
+    atomicOr(&flags[0], (minus128 ? 1u : 0u) | (payload_bad ? 2u : 0u));
+  }
+  __syncthreads();
+
+  // The checks of state_capsule.cpp:497-576 in their order; every value here
+  // is uniform over the workgroup and the first failure names the outcome.
   uint32_t result = GDN_STATE_CODEC_CAPSULE_OK;
   uint32_t count = 0;
-  if (content < kResidualOffset) {
+  if (!has_header) {
     result = GDN_STATE_CODEC_CAPSULE_TRUNCATED;  // geometry digest truncated (:509-511)
   } else {
-    if (t < static_cast<int>(kHeaderWords)) {
-      header[t] = reinterpret_cast<const uint32_t*>(base)[t];
-    }
-    __syncthreads();
     count = header[13];
+    bool same = header[7] == static_cast<uint32_t>(a.identity.generation) &&
+                header[8] == static_cast<uint32_t>(a.identity.generation >> 32) &&
+                header[9] == static_cast<uint32_t>(a.identity.epoch) &&
+                header[10] == static_cast<uint32_t>(a.identity.epoch >> 32) &&
+                header[11] == kDim && header[12] == kDim;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) same = same && header[14 + i] == a.identity.geometry[i];
     if (header[2] != 1 || header[3] != kWindow || header[4] != kRank || header[5] != 8 ||
         !(__uint_as_float(header[6]) == kSmoothingFloor)) {
       result = GDN_STATE_CODEC_CAPSULE_PARAMETERS;
+    } else if (!same) {
+      result = GDN_STATE_CODEC_CAPSULE_IDENTITY;
+    } else if (count >= kWindow) {  // rank 4 <= min(128, 128) always holds
+      result = GDN_STATE_CODEC_CAPSULE_POSITION;
+    } else if (count != a.expected_positions[s]) {
+      result = GDN_STATE_CODEC_CAPSULE_PHASE;
+    } else if (!has_codes) {
+      result = GDN_STATE_CODEC_CAPSULE_TRUNCATED;
+    } else if (flags[0] & 1u) {
+      result = GDN_STATE_CODEC_CAPSULE_RESIDUAL_DOMAIN;
+    } else if (!has_payload) {
+      result = GDN_STATE_CODEC_CAPSULE_TRUNCATED;
+    } else if (flags[0] & 2u) {
+      result = GDN_STATE_CODEC_CAPSULE_BOUNDARY_PAYLOAD;
     } else {
-      bool same = header[7] == static_cast<uint32_t>(a.identity.generation) &&
-                  header[8] == static_cast<uint32_t>(a.identity.generation >> 32) &&
-                  header[9] == static_cast<uint32_t>(a.identity.epoch) &&
-                  header[10] == static_cast<uint32_t>(a.identity.epoch >> 32) &&
-                  header[11] == kDim && header[12] == kDim;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) same = same && header[14 + i] == a.identity.geometry[i];
-      if (!same) {
-        result = GDN_STATE_CODEC_CAPSULE_IDENTITY;
-      } else if (count >= kWindow) {  // rank 4 <= min(128, 128) always holds
-        result = GDN_STATE_CODEC_CAPSULE_POSITION;
-      } else if (count != a.expected_positions[s]) {
-        result = GDN_STATE_CODEC_CAPSULE_PHASE;
-      } else if (content - kResidualOffset < static_cast<uint32_t>(kTile)) {
+      // Records (:562-570): each is read whole, then checked; the first
+      // record that runs past the content ends the restore as truncated.
+      const uint32_t present = whole < count ? whole : count;
+      if (flags[1] & ((1u << present) - 1u)) {
+        result = GDN_STATE_CODEC_CAPSULE_RECORD_NONFINITE;
+      } else if (present < count) {
         result = GDN_STATE_CODEC_CAPSULE_TRUNCATED;
+      } else if (content != content_bytes(count)) {
+        result = GDN_STATE_CODEC_CAPSULE_TRAILING;
       }
     }
   }
@@ -569,69 +655,7 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
     if (t == 0) a.status[s] = result;
     return;
   }
-  // Codes: thread t holds 8-byte words w = i * 256 + t of the [key][value] tile.
-  uint64_t codes[8];
-  bool bad = false;
-  const uint64_t* code_words = reinterpret_cast<const uint64_t*>(base + kResidualOffset);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    codes[i] = code_words[i * kThreads + t];
-    bad = bad || has_byte_0x80(codes[i]);
-  }
-  if (__syncthreads_or(bad)) {
-    if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_RESIDUAL_DOMAIN;
-    return;
-  }
-  if (content < kRecordsOffset) {
-    if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_TRUNCATED;
-    return;
-  }
-  // Boundary payload (:550-561).
-  {
-    const float value = *reinterpret_cast<const float*>(base + kSmoothingOffset + 4 * t);
-    if (t < kDim) {
-      sm[t] = value;
-      bad = !(isfinite(value) && value > 0.0f);
-    } else {
-      sc[t - kDim] = value;
-      bad = !(isfinite(value) && value >= 0.0f);
-    }
-    const float2 k2 = reinterpret_cast<const float2*>(base + kCompKeysOffset)[t];
-    const float2 v2 = reinterpret_cast<const float2*>(base + kCompValuesOffset)[t];
-    ck[2 * t] = k2.x;
-    ck[2 * t + 1] = k2.y;
-    cv[2 * t] = v2.x;
-    cv[2 * t + 1] = v2.y;
-    bad = bad || !isfinite(k2.x) || !isfinite(k2.y) || !isfinite(v2.x) || !isfinite(v2.y);
-  }
-  if (__syncthreads_or(bad)) {
-    if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_BOUNDARY_PAYLOAD;
-    return;
-  }
-  // Records (:562-570): each is read whole, then checked; the first record
-  // that runs past the content ends the restore as truncated.
-  const uint32_t whole = (content - kRecordsOffset) / kRecordBytes;
-  const uint32_t present = whole < count ? whole : count;
-  {
-    const float* src = reinterpret_cast<const float*>(base + kRecordsOffset);
-    for (uint32_t w = t; w < kRecordFloats * present; w += kThreads) {
-      const float value = src[w];
-      rec[w] = value;
-      bad = bad || !isfinite(value);
-    }
-  }
-  if (__syncthreads_or(bad)) {
-    if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_RECORD_NONFINITE;
-    return;
-  }
-  if (present < count) {
-    if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_TRUNCATED;
-    return;
-  }
-  if (content != content_bytes(count)) {
-    if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_TRAILING;
-    return;
-  }
+
   // DenseState (:337-352) must be finite.  A magnitude bound decides it for
   // almost every capsule: with B0 = max|s| max|scale| + 4 max|ck| max|cv| and
   // Bj = max|decay_j| B(j-1) + max|key_j| max|corr_j|, every value the
@@ -640,34 +664,14 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
   // FLT_MAX (1 - 2^-10) prove the state finite.  Otherwise it is evaluated
   // exactly, in its own order: ((s*code)/127)*scale, + ck.cv over the rank,
   // then decay*x + key*corr per record (the build disables contraction).
-  {
-    const int wave = t >> 6, lane = t & 63;
-    // Vector 0 smoothing, 1 scales, 2 ck, 3 cv, 4 + 3j + {0, 1, 2} record j.
-    for (uint32_t vec = wave; vec < 4 + 3 * count; vec += kThreads / 64) {
-      float m = 0.0f;
-      if (vec < 2) {
-        const float* src = vec == 0 ? sm : sc;
-        m = fmaxf(fabsf(src[lane]), fabsf(src[lane + 64]));
-      } else if (vec < 4) {
-        const float* src = vec == 2 ? ck : cv;
-        for (int i = lane; i < kDim * kRank; i += 64) m = fmaxf(m, fabsf(src[i]));
-      } else {
-        const float* src = rec + (vec - 4) * kDim;
-        m = fmaxf(fabsf(src[lane]), fabsf(src[lane + 64]));
-      }
-      m = wave_max(m);
-      if (lane == 0) maxima[vec] = m;
-    }
-  }
-  __syncthreads();
-  double bound = static_cast<double>(maxima[0]) * maxima[1] +
-                 4.0 * static_cast<double>(maxima[2]) * maxima[3];
+  const auto mx = [&](int slot) { return static_cast<double>(__uint_as_float(maxima[slot])); };
+  double bound = mx(0) * mx(1) + 4.0 * mx(2) * mx(3);
   for (uint32_t j = 0; j < count; ++j) {
-    bound = static_cast<double>(maxima[4 + 3 * j]) * bound +
-            static_cast<double>(maxima[5 + 3 * j]) * maxima[6 + 3 * j];
+    bound = mx(4 + 3 * j) * bound + mx(5 + 3 * j) * mx(6 + 3 * j);
   }
   const double limit = static_cast<double>(FLT_MAX) * (1.0 - 1.0 / 1024.0);
-  if (!(bound < limit && static_cast<double>(maxima[0]) * 127.0 < limit)) {
+  bool bad = false;
+  if (!(bound < limit && mx(0) * 127.0 < limit)) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int w = i * kThreads + t;
@@ -689,14 +693,14 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
 #pragma unroll
       for (int b = 0; b < 8; ++b) bad = bad || !isfinite(x[b]);
     }
-  }
-  if (__syncthreads_or(bad)) {
-    if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_STATE_NONFINITE;
-    return;
+    if (__syncthreads_or(bad)) {
+      if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_STATE_NONFINITE;
+      return;
+    }
   }
   // The slot's format: one gate per record, fp16 compensators and records.
-  bad = !half_exact(ck[2 * t]) || !half_exact(ck[2 * t + 1]) || !half_exact(cv[2 * t]) ||
-        !half_exact(cv[2 * t + 1]);
+  bad = !half_exact(key_pair.x) || !half_exact(key_pair.y) || !half_exact(value_pair.x) ||
+        !half_exact(value_pair.y);
   for (uint32_t w = t; w < kRecordFloats * count; w += kThreads) {
     const uint32_t j = w / kRecordFloats, i = w - j * kRecordFloats;
     const float value = rec[w];
@@ -744,9 +748,9 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
   {
     const uint64_t comp_base = static_cast<uint64_t>(s) * kDim * kRank;
     reinterpret_cast<uint32_t*>(a.comp_keys + comp_base)[t] =
-        float_to_half_bits(ck[2 * t]) | (float_to_half_bits(ck[2 * t + 1]) << 16);
+        float_to_half_bits(key_pair.x) | (float_to_half_bits(key_pair.y) << 16);
     reinterpret_cast<uint32_t*>(a.comp_values + comp_base)[t] =
-        float_to_half_bits(cv[2 * t]) | (float_to_half_bits(cv[2 * t + 1]) << 16);
+        float_to_half_bits(value_pair.x) | (float_to_half_bits(value_pair.y) << 16);
   }
   const uint64_t record_base = static_cast<uint64_t>(s) * kWindow;
   if (static_cast<uint32_t>(t) < count) {
