@@ -358,12 +358,16 @@ def bench_refit(steps: int, warmup: int):
             t.copy_((torch.randn(t.shape, device=dev, generator=gen) * 0.02).to(torch.float16))
         slot.record_decay.uniform_(0.93, 0.99, generator=gen)
         nxt = WindowSlot.allocate(states, dev)
-        copies.append((slot, nxt))
+        # The power refit clears the window it folds; every launch gets the
+        # full window back (outside the timed events).
+        saved = (slot.record_decay.clone(), slot.record_keys.clone(),
+                 slot.record_corrections.clone())
+        copies.append((slot, nxt, saved))
     workspace = torch.empty((states, 128, 128), dtype=torch.float32, device=dev)
     lib, stream = native(), torch.cuda.current_stream().cuda_stream
 
     def refit(r, power):
-        slot, nxt = copies[r]
+        slot, nxt, _ = copies[r]
         return lib.window_boundary_launch_v1(
             stream, *slot.pointers(), nxt.residual.data_ptr(), nxt.smoothing.data_ptr(),
             nxt.scales.data_ptr(), nxt.compensator_keys.data_ptr(),
@@ -374,7 +378,12 @@ def bench_refit(steps: int, warmup: int):
         pairs = []
         for i in range(max(warmup, 1) * ROTATIONS + steps):
             r = i % ROTATIONS
-            copies[r][0].positions[:, 0] = 16  # a full window (the power refit clears it)
+            slot, _, saved = copies[r]
+            slot.positions[:, 0] = 16  # a full window (the power refit clears it)
+            if power:
+                for dst, src in zip((slot.record_decay, slot.record_keys,
+                                     slot.record_corrections), saved):
+                    dst.copy_(src)
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             assert refit(r, power) == 0
