@@ -168,39 +168,63 @@ __global__ __launch_bounds__(kThreads, 8) void decode_projection_kernel(
 
 // ----------------------------------------------------------------- chunked
 
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 
-// Three-way bf16 split of a pair of fp32 values: w = hi + mid + lo, each part
-// rounded to nearest even by v_cvt_pk_bf16_f32; the remainders w - hi and
-// (w - hi) - mid are exact in fp32, so the parts carry all 24 significand bits.
-__device__ __forceinline__ void split3_pair(float w0, float w1, uint32_t& hi,
-                                            uint32_t& mid, uint32_t& lo) {
-  const bf16x2 h = {static_cast<__bf16>(w0), static_cast<__bf16>(w1)};
-  const float r0 = w0 - static_cast<float>(h[0]);
-  const float r1 = w1 - static_cast<float>(h[1]);
-  const bf16x2 m = {static_cast<__bf16>(r0), static_cast<__bf16>(r1)};
-  const float t0 = r0 - static_cast<float>(m[0]);
-  const float t1 = r1 - static_cast<float>(m[1]);
-  const bf16x2 l = {static_cast<__bf16>(t0), static_cast<__bf16>(t1)};
-  hi = __builtin_bit_cast(uint32_t, h);
-  mid = __builtin_bit_cast(uint32_t, m);
-  lo = __builtin_bit_cast(uint32_t, l);
+// Upper halves of two fp32 bit patterns packed as a bf16 pair (low element
+// first): one byte permute.
+__device__ __forceinline__ uint32_t upper_halves(uint32_t first, uint32_t second) {
+  return __builtin_amdgcn_perm(second, first, 0x07060302u);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16_of_codes(uint32_t word, int pair) {
-  // bf16 of an int8 code is the upper half of its exact fp32 value.
-  const uint32_t a = __float_as_uint(code_byte(word, 2 * pair));
-  const uint32_t b = __float_as_uint(code_byte(word, 2 * pair + 1));
-  return (a >> 16) | (b & 0xFFFF0000u);
+// Three-way bf16 split of a pair of fp32 values, w = hi + mid + lo exactly,
+// by truncation: hi keeps the sign, exponent and top 7 fraction bits of w;
+// the remainder r = w - hi is exact in fp32 and has at most 16 significant
+// bits; mid keeps the top 8 of those and lo = r - mid, exact, has at most 8,
+// so every part is a bf16 value (the upper half of its fp32 pattern).
+__device__ __forceinline__ void split3_pair(float w0, float w1, uint32_t& hi,
+                                            uint32_t& mid, uint32_t& lo) {
+  constexpr uint32_t kUpper = 0xFFFF0000u;
+  const uint32_t h0 = __float_as_uint(w0) & kUpper;
+  const uint32_t h1 = __float_as_uint(w1) & kUpper;
+  const float r0 = w0 - __uint_as_float(h0);
+  const float r1 = w1 - __uint_as_float(h1);
+  const uint32_t m0 = __float_as_uint(r0) & kUpper;
+  const uint32_t m1 = __float_as_uint(r1) & kUpper;
+  const float t0 = r0 - __uint_as_float(m0);
+  const float t1 = r1 - __uint_as_float(m1);
+  hi = upper_halves(h0, h1);
+  mid = upper_halves(m0, m1);
+  lo = upper_halves(__float_as_uint(t0), __float_as_uint(t1));
+}
+
+// bf16 pair of the signed bytes 2*kPair, 2*kPair+1 of `word` (low element
+// first).  bf16 of an int8 code is the upper half of its exact fp32 value: two
+// SDWA conversions select and sign-extend the bytes in the operand read, and
+// one byte permute packs the two upper halves.  One asm block keeps a single
+// temporary live per pair.
+template <int kPair>
+__device__ __forceinline__ uint32_t bf16_pair_of_codes(uint32_t word) {
+  uint32_t packed, low;
+  if constexpr (kPair == 0) {
+    asm("v_cvt_f32_i32_sdwa %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f32_i32_sdwa %0, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_perm_b32 %0, %0, %1, %3"
+        : "=&v"(packed), "=&v"(low) : "v"(word), "s"(0x07060302u));
+  } else {
+    asm("v_cvt_f32_i32_sdwa %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f32_i32_sdwa %0, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+        "v_perm_b32 %0, %0, %1, %3"
+        : "=&v"(packed), "=&v"(low) : "v"(word), "s"(0x07060302u));
+  }
+  return packed;
 }
 
 __device__ __forceinline__ bf16x8 codes_to_bf16x8(uint32_t w0, uint32_t w1) {
   uint4 packed;
-  packed.x = pack_bf16_of_codes(w0, 0);
-  packed.y = pack_bf16_of_codes(w0, 1);
-  packed.z = pack_bf16_of_codes(w1, 0);
-  packed.w = pack_bf16_of_codes(w1, 1);
+  packed.x = bf16_pair_of_codes<0>(w0);
+  packed.y = bf16_pair_of_codes<1>(w0);
+  packed.z = bf16_pair_of_codes<0>(w1);
+  packed.w = bf16_pair_of_codes<1>(w1);
   return __builtin_bit_cast(bf16x8, packed);
 }
 
@@ -227,6 +251,7 @@ __global__ __launch_bounds__(kThreads, kLayout == kValueKey ? 8 : 4) void chunke
   constexpr int kBlockTokens = 16;
   __shared__ uint4 a_lds[3][4][64];  // [split][k-step][lane] x 8 bf16
   __shared__ float s_lds[kDim];
+  __shared__ __align__(16) float e_lds[kDim];  // scale[v] / 127
 
   const uint64_t pair = blockIdx.x;  // sequence * value_heads + head
   const uint64_t n = pair / value_heads;
@@ -270,12 +295,10 @@ __global__ __launch_bounds__(kThreads, kLayout == kValueKey ? 8 : 4) void chunke
       }
     }
   }
-  float epilogue[2];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    epilogue[c] = scales[pair * kDim + 32 * wave + 16 * c + col] / kQuantizedMaximum;
+  if (t < kDim) {
+    s_lds[t] = smoothing[pair * kDim + t];
+    e_lds[t] = scales[pair * kDim + t] / kQuantizedMaximum;
   }
-  if (t < kDim) s_lds[t] = smoothing[pair * kDim + t];
 
   // Producer role: thread t builds token row m = t / 16 of the block, keys
   // 8*kc..+7 (kc = t % 16), which is k-step kc % 4 of lane group kc / 4.
@@ -323,15 +346,38 @@ __global__ __launch_bounds__(kThreads, kLayout == kValueKey ? 8 : 4) void chunke
         }
       }
     }
+    // Accumulator r of column tile c is token row 4g + r of the block, value
+    // 32 wave + 16 c + col.  Adjacent lanes swap one value (DPP quad_perm
+    // [1,0,3,2]) so that the even lane of a pair holds values col, col + 1 of
+    // tile 0 and the odd lane values col - 1, col of tile 1: each store then
+    // writes the wave's 32 values of a row as one whole 128-byte line.
+    const bool odd = (col & 1) != 0;
+    const int first = 32 * wave + (odd ? 15 + col : col);
+    const float2 factor = *reinterpret_cast<const float2*>(&e_lds[first]);
+    const uint64_t row_stride = static_cast<uint64_t>(value_heads) * kDim;
+    float* const lane_out = out + ((n * tokens + block) * value_heads + h) * kDim +
+                            4 * g * row_stride + first;
+    uint2 pairs[4];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int v = 32 * wave + 16 * c + col;
+    for (int r = 0; r < 4; ++r) {
+      const float send = odd ? acc[0][r] : acc[1][r];
+      const float got = __builtin_bit_cast(
+          float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, send), 0xB1, 0xF, 0xF,
+                                             false));
+      const float lo = odd ? got : acc[0][r];
+      const float hi = odd ? acc[1][r] : got;
+      pairs[r] = make_uint2(__float_as_uint(lo * factor.x), __float_as_uint(hi * factor.y));
+    }
+    if (block + kBlockTokens <= tokens) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const uint32_t row_token = block + 4 * g + r;
-        if (row_token < tokens) {
-          stream_store(out + ((n * tokens + row_token) * value_heads + h) * kDim + v,
-                       acc[c][r] * epilogue[c]);
+        stream_store(reinterpret_cast<uint2*>(lane_out + r * row_stride), pairs[r]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (block + 4 * g + r < tokens) {
+          stream_store(reinterpret_cast<uint2*>(lane_out + r * row_stride), pairs[r]);
         }
       }
     }
