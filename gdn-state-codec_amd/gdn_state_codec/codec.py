@@ -168,18 +168,25 @@ def _projection_inputs(codes, smoothing, scales, queries, heads_dim: int):
 
 def project_decode(codes: torch.Tensor, smoothing: torch.Tensor, scales: torch.Tensor,
                    queries: torch.Tensor, query_scale: float = 1.0,
-                   layout: int = LAYOUT_VALUE_KEY, out=None) -> torch.Tensor:
+                   layout: int = LAYOUT_VALUE_KEY, out=None,
+                   validate: bool = True) -> torch.Tensor:
     """o[b,h,v] = sum_k code(v,k) s[k] (query_scale q[b, h*Hq/H, k]) / 127 * scale[v].
 
-    codes [B,H,128,128] int8; queries [B,Hq,128] bf16; returns fp32 [B,H,128]."""
-    value_heads, query_heads = _projection_inputs(codes, smoothing, scales, queries, 1)
+    codes [B,H,128,128] int8; queries [B,Hq,128] bf16; returns fp32 [B,H,128].
+    `validate=False` skips the tensor checks for callers that already made them
+    on the same buffers (a decode loop); the library still checks its arguments."""
     batch = codes.shape[0]
-    _require(queries.dim() == 3 and queries.shape[0] == batch,
-             "GDN State Codec decode queries must be [B,Hq,128]")
+    if validate:
+        value_heads, query_heads = _projection_inputs(codes, smoothing, scales, queries, 1)
+        _require(queries.dim() == 3 and queries.shape[0] == batch,
+                 "GDN State Codec decode queries must be [B,Hq,128]")
+    else:
+        value_heads, query_heads = codes.shape[1], queries.shape[1]
     if out is None:
         out = torch.empty((batch, value_heads, DIM), dtype=torch.float32, device=codes.device)
-    _require(out.is_contiguous() and out.dtype == torch.float32
-             and out.numel() == batch * value_heads * DIM, "output geometry differs")
+    if validate:
+        _require(out.is_contiguous() and out.dtype == torch.float32
+                 and out.numel() == batch * value_heads * DIM, "output geometry differs")
     _check(native().encoded_projection_decode_launch_v4(
         _stream(), codes.data_ptr(), smoothing.data_ptr(), scales.data_ptr(),
         queries.data_ptr(), out.data_ptr(), batch, value_heads, query_heads,
@@ -189,20 +196,26 @@ def project_decode(codes: torch.Tensor, smoothing: torch.Tensor, scales: torch.T
 
 def project_chunked(codes: torch.Tensor, smoothing: torch.Tensor, scales: torch.Tensor,
                     queries: torch.Tensor, query_scale: float = 1.0,
-                    layout: int = LAYOUT_VALUE_KEY, out=None) -> torch.Tensor:
+                    layout: int = LAYOUT_VALUE_KEY, out=None,
+                    validate: bool = True) -> torch.Tensor:
     """Chunked projection of T query tokens per sequence against each sequence's state.
 
-    codes [N,H,128,128] int8; queries [N,T,Hq,128] bf16; returns fp32 [N,T,H,128]."""
-    value_heads, query_heads = _projection_inputs(codes, smoothing, scales, queries, 2)
+    codes [N,H,128,128] int8; queries [N,T,Hq,128] bf16; returns fp32 [N,T,H,128].
+    `validate=False` skips the tensor checks, as for project_decode."""
     seqs = codes.shape[0]
-    _require(queries.dim() == 4 and queries.shape[0] == seqs,
-             "GDN State Codec chunked queries must be [N,T,Hq,128]")
+    if validate:
+        value_heads, query_heads = _projection_inputs(codes, smoothing, scales, queries, 2)
+        _require(queries.dim() == 4 and queries.shape[0] == seqs,
+                 "GDN State Codec chunked queries must be [N,T,Hq,128]")
+    else:
+        value_heads, query_heads = codes.shape[1], queries.shape[2]
     tokens = queries.shape[1]
     if out is None:
         out = torch.empty((seqs, tokens, value_heads, DIM), dtype=torch.float32,
                           device=codes.device)
-    _require(out.is_contiguous() and out.dtype == torch.float32
-             and out.numel() == seqs * tokens * value_heads * DIM, "output geometry differs")
+    if validate:
+        _require(out.is_contiguous() and out.dtype == torch.float32
+                 and out.numel() == seqs * tokens * value_heads * DIM, "output geometry differs")
     _check(native().encoded_projection_chunked_launch_v4(
         _stream(), codes.data_ptr(), smoothing.data_ptr(), scales.data_ptr(),
         queries.data_ptr(), out.data_ptr(), seqs, tokens, value_heads, query_heads,

@@ -125,3 +125,15 @@ def test_chunked_equals_decode_token_by_token(device):
                                          1.0, VK))
         assert _within(dec, out64[:, t], bound[:, t]).all()
         assert _within(chunked[:, t], out64[:, t], bound[:, t]).all()
+
+
+def test_projection_without_checks_is_identical(device):
+    """`validate=False` only skips the host-side tensor checks."""
+    codes, s, sc = _encoded((2, 8), 80, VK)
+    g = [to_gpu(a, device) for a in (codes, s, sc)]
+    qd = to_gpu(_queries((2, 4, 128), 81), device).view(torch.bfloat16)
+    qc = to_gpu(_queries((2, 7, 4, 128), 82), device).view(torch.bfloat16)
+    assert torch.equal(codec.project_decode(*g, qd, 0.5, VK),
+                       codec.project_decode(*g, qd, 0.5, VK, validate=False))
+    assert torch.equal(codec.project_chunked(*g, qc, 0.5, VK),
+                       codec.project_chunked(*g, qc, 0.5, VK, validate=False))
