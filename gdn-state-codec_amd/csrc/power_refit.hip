@@ -15,8 +15,11 @@
 // operator in parallel, one row or column per thread; projections and norms
 // on single threads, broadcast through LDS), so the result is bit-identical to
 // the CPU statement of the reference kernel.  One 128-thread workgroup per
-// state, operands staged in LDS; the codes use a 132-byte row stride so both
-// the row walk and the column walk are free of bank conflicts.
+// state, operands staged in LDS: the codes at a 132-byte row stride so both
+// the row walk and the column walk are free of bank conflicts, compensators
+// and records as fp16 bits, and a 256-entry table of code / 127.  The fitted
+// residual is evaluated once per cell into the workspace, which the smoothing,
+// scale and code passes then read back.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -51,18 +54,27 @@ struct PowerArgs {
   uint32_t power_iterations;
 };
 
+// Compensators and records are fp16 values (the fitted ranks are rounded to
+// fp16 when formed), so they are kept as fp16 bits and widened exactly when
+// read: 32,424 bytes, five workgroups per CU.
 struct PowerShared {
   int8_t code[kDim * kCodeStride];  // [value column][key row]
-  float ck[kDim * kRank], cv[kDim * kRank];
-  float nk[kDim * kRank], nv[kDim * kRank];
-  float rk[kWindow * kDim], rc[kWindow * kDim];
-  float smoothing[kDim], scales[kDim], next_smoothing[kDim];
-  float left[kDim], right[kDim];
+  uint16_t ck[kDim * kRank], cv[kDim * kRank];
+  uint16_t nk[kDim * kRank], nv[kDim * kRank];
+  uint16_t rk[kWindow * kDim], rc[kWindow * kDim];
+  float smoothing[kDim], scales[kDim];
+  union {
+    float left[kDim];            // power iteration
+    float next_smoothing[kDim];  // re-encoding, after the iteration
+  };
+  float right[kDim];
   float old_projection[kRank], fitted_projection[kRank], record_projection[kWindow];
   float record_suffix[kWindow];
   float scalar;  // norm inverse / singular value broadcast
   int flag;
+  float code_value[256];  // code / 127 by the code's byte pattern
 };
+static_assert(sizeof(PowerShared) <= 163840 / 5, "five workgroups per CU");
 
 // window_boundary.cpp:17-23.
 __device__ __forceinline__ float newton_sqrt(float value) {
@@ -80,8 +92,10 @@ __device__ __forceinline__ float h2f(uint16_t h) { return half_bits_to_float(h);
 __device__ __forceinline__ float code_over_127(int8_t code) {
   return div_by_reciprocal(static_cast<float>(code), kQuantizedMaximum, kInvQuantizedMaximum);
 }
-__device__ __forceinline__ float round_half(float x) {
-  return half_bits_to_float(float_to_half_bits(x));
+// code / 127 from the workgroup's table: one LDS read instead of the four
+// instructions of the exact division.
+__device__ __forceinline__ float code_value(const PowerShared& sh, int8_t code) {
+  return sh.code_value[static_cast<uint8_t>(code)];
 }
 
 // Normalize (:25-37) of v; returns whether the norm was usable.  The squared
@@ -100,25 +114,32 @@ __device__ bool normalize(PowerShared& sh, float* v, int t) {
   return ok;
 }
 
-// Projections of an apply: old compensator side, records, fitted ranks; one
-// sequential sum per thread in the reference's loop order.
-__device__ void projections(PowerShared& sh, const float* vector, const float* old_basis,
-                            const float* record_basis, const float* fitted_basis,
+// Projections of an apply (old compensator side, records, fitted ranks): one
+// sequential sum per thread in the reference's loop order.  Wavefront 0 runs
+// the compensator sides (lanes 0..3 the old ranks, lanes 4..7 the fitted
+// ones: the same loop over a per-lane basis, so no branch divergence) while
+// wavefront 1 runs the 16 record sides (its lanes 0..15).
+__device__ void projections(PowerShared& sh, const float* vector, const uint16_t* old_basis,
+                            const uint16_t* record_basis, const uint16_t* fitted_basis,
                             int fitted, int t) {
-  if (t < kRank) {
+  if (t < 2 * kRank) {
+    const int r = t & (kRank - 1);
+    const bool is_fitted = t >= kRank;
+    if (!is_fitted || r < fitted) {
+      const uint16_t* basis = is_fitted ? fitted_basis : old_basis;
+      float acc = 0.0f;
+      for (int i = 0; i < kDim; ++i) acc += h2f(basis[i * kRank + r]) * vector[i];
+      if (is_fitted) {
+        sh.fitted_projection[r] = acc;
+      } else {
+        sh.old_projection[r] = acc;
+      }
+    }
+  } else if (t >= 64 && t < 64 + kWindow) {
+    const int j = t - 64;
     float acc = 0.0f;
-    for (int i = 0; i < kDim; ++i) acc += old_basis[i * kRank + t] * vector[i];
-    sh.old_projection[t] = acc;
-  } else if (t < kRank + kWindow) {
-    const int j = t - kRank;
-    float acc = 0.0f;
-    for (int i = 0; i < kDim; ++i) acc += record_basis[j * kDim + i] * vector[i];
+    for (int i = 0; i < kDim; ++i) acc += h2f(record_basis[j * kDim + i]) * vector[i];
     sh.record_projection[j] = acc;
-  } else if (t < 2 * kRank + kWindow && t - kRank - kWindow < fitted) {
-    const int r = t - kRank - kWindow;
-    float acc = 0.0f;
-    for (int i = 0; i < kDim; ++i) acc += fitted_basis[i * kRank + r] * vector[i];
-    sh.fitted_projection[r] = acc;
   }
   __syncthreads();
 }
@@ -131,14 +152,14 @@ __device__ void apply_right(PowerShared& sh, const float* vector, float* output,
   float value = 0.0f;
   const float s = sh.smoothing[row];
   for (int column = 0; column < kDim; ++column) {
-    value += code_over_127(sh.code[column * kCodeStride + row]) * s * sh.scales[column] *
+    value += code_value(sh, sh.code[column * kCodeStride + row]) * s * sh.scales[column] *
              vector[column] * bs;
   }
-  for (int r = 0; r < kRank; ++r) value += sh.ck[row * kRank + r] * sh.old_projection[r] * bs;
+  for (int r = 0; r < kRank; ++r) value += h2f(sh.ck[row * kRank + r]) * sh.old_projection[r] * bs;
   for (int j = 0; j < kWindow; ++j) {
-    value += sh.rk[j * kDim + row] * sh.record_projection[j] * sh.record_suffix[j];
+    value += h2f(sh.rk[j * kDim + row]) * sh.record_projection[j] * sh.record_suffix[j];
   }
-  for (int r = 0; r < fitted; ++r) value -= sh.nk[row * kRank + r] * sh.fitted_projection[r];
+  for (int r = 0; r < fitted; ++r) value -= h2f(sh.nk[row * kRank + r]) * sh.fitted_projection[r];
   __syncthreads();  // every thread has read `vector` before it may be overwritten
   output[row] = value;
   __syncthreads();
@@ -153,13 +174,13 @@ __device__ void apply_transpose(PowerShared& sh, const float* vector, float* out
   const float scale = sh.scales[column];
   const int8_t* code = sh.code + column * kCodeStride;
   for (int row = 0; row < kDim; ++row) {
-    value += code_over_127(code[row]) * sh.smoothing[row] * scale * vector[row] * bs;
+    value += code_value(sh, code[row]) * sh.smoothing[row] * scale * vector[row] * bs;
   }
-  for (int r = 0; r < kRank; ++r) value += sh.cv[column * kRank + r] * sh.old_projection[r] * bs;
+  for (int r = 0; r < kRank; ++r) value += h2f(sh.cv[column * kRank + r]) * sh.old_projection[r] * bs;
   for (int j = 0; j < kWindow; ++j) {
-    value += sh.rc[j * kDim + column] * sh.record_projection[j] * sh.record_suffix[j];
+    value += h2f(sh.rc[j * kDim + column]) * sh.record_projection[j] * sh.record_suffix[j];
   }
-  for (int r = 0; r < fitted; ++r) value -= sh.nv[column * kRank + r] * sh.fitted_projection[r];
+  for (int r = 0; r < fitted; ++r) value -= h2f(sh.nv[column * kRank + r]) * sh.fitted_projection[r];
   __syncthreads();
   output[column] = value;
   __syncthreads();
@@ -168,14 +189,14 @@ __device__ void apply_transpose(PowerShared& sh, const float* vector, float* out
 // ResidualCell (:223-251).
 __device__ __forceinline__ float residual_cell(const PowerShared& sh, int row, int column,
                                                float bs) {
-  float value = code_over_127(sh.code[column * kCodeStride + row]) * sh.smoothing[row] *
+  float value = code_value(sh, sh.code[column * kCodeStride + row]) * sh.smoothing[row] *
                 sh.scales[column] * bs;
   for (int r = 0; r < kRank; ++r) {
-    value += sh.ck[row * kRank + r] * sh.cv[column * kRank + r] * bs;
-    value -= sh.nk[row * kRank + r] * sh.nv[column * kRank + r];
+    value += h2f(sh.ck[row * kRank + r]) * h2f(sh.cv[column * kRank + r]) * bs;
+    value -= h2f(sh.nk[row * kRank + r]) * h2f(sh.nv[column * kRank + r]);
   }
   for (int j = 0; j < kWindow; ++j) {
-    value += sh.rk[j * kDim + row] * sh.rc[j * kDim + column] * sh.record_suffix[j];
+    value += h2f(sh.rk[j * kDim + row]) * h2f(sh.rc[j * kDim + column]) * sh.record_suffix[j];
   }
   return value;
 }
@@ -196,17 +217,19 @@ __global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
     *reinterpret_cast<uint32_t*>(&sh.code[column * kCodeStride + row]) = w;
   }
   for (int i = t; i < kDim * kRank; i += kThreads) {
-    sh.ck[i] = h2f(a.comp_keys[vb * kRank + i]);
-    sh.cv[i] = h2f(a.comp_values[vb * kRank + i]);
-    sh.nk[i] = 0.0f;
-    sh.nv[i] = 0.0f;
+    sh.ck[i] = a.comp_keys[vb * kRank + i];
+    sh.cv[i] = a.comp_values[vb * kRank + i];
+    sh.nk[i] = 0u;
+    sh.nv[i] = 0u;
   }
   for (int i = t; i < kWindow * kDim; i += kThreads) {
-    sh.rk[i] = h2f(a.record_keys[rb * kDim + i]);
-    sh.rc[i] = h2f(a.record_corrections[rb * kDim + i]);
+    sh.rk[i] = a.record_keys[rb * kDim + i];
+    sh.rc[i] = a.record_corrections[rb * kDim + i];
   }
   sh.smoothing[t] = a.smoothing[vb + t];
   sh.scales[t] = a.scales[vb + t];
+  sh.code_value[t] = code_over_127(static_cast<int8_t>(t));
+  sh.code_value[t + kThreads] = code_over_127(static_cast<int8_t>(t + kThreads));
   // BuildSuffix (:102-111), computed identically by every thread.
   float bs = 1.0f;
   for (int j = kWindow - 1; j >= 0; --j) {
@@ -236,21 +259,36 @@ __global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
     const float singular = sh.scalar;
     if (singular > 1.0e-20f) {
       const float inverse = 1.0f / singular;
-      sh.nk[t * kRank + rank] = round_half(sh.left[t] * inverse * singular);
-      sh.nv[t * kRank + rank] = round_half(sh.right[t]);
+      sh.nk[t * kRank + rank] = static_cast<uint16_t>(float_to_half_bits(sh.left[t] * inverse * singular));
+      sh.nv[t * kRank + rank] = static_cast<uint16_t>(float_to_half_bits(sh.right[t]));
     }
     __syncthreads();
   }
 
-  // ---- residual, fresh smoothing (row t), workspace ---------------------------
+  // ---- residual (column t) into the workspace ---------------------------------
+  // Each cell of R minus the fit is evaluated once, stored coalesced (lanes
+  // hold consecutive values), and read back by the three passes that follow;
+  // the reads return the same fp32 bits the evaluation would.
+  float* const work = a.workspace + state * kTile;  // [key row][value column]
+  {
+    const int column = t;
+    for (int row = 0; row < kDim; ++row) {
+      work[row * kDim + column] = residual_cell(sh, row, column, bs);
+    }
+  }
+  __syncthreads();  // the workspace writes are visible to the whole workgroup
+
+  // ---- fresh smoothing (row t): sequential sum of |cell| over the columns ----
   {
     const int row = t;
+    const float4* cells = reinterpret_cast<const float4*>(work + row * kDim);
     float mean_absolute = 0.0f;
-    float* work = a.workspace + state * kTile + static_cast<uint64_t>(row) * kDim;
-    for (int column = 0; column < kDim; ++column) {
-      const float value = residual_cell(sh, row, column, bs);
-      work[column] = value;
-      mean_absolute += fabsf(value);
+    for (int q = 0; q < kDim / 4; ++q) {
+      const float4 c = cells[q];
+      mean_absolute += fabsf(c.x);
+      mean_absolute += fabsf(c.y);
+      mean_absolute += fabsf(c.z);
+      mean_absolute += fabsf(c.w);
     }
     const float mean = mean_absolute / 128.0f;
     const float s = newton_sqrt(mean > kBoundaryFloor ? mean : kBoundaryFloor);
@@ -264,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
     const int column = t;
     float maximum = 0.0f;
     for (int row = 0; row < kDim; ++row) {
-      const float value = fabsf(residual_cell(sh, row, column, bs) / sh.next_smoothing[row]);
+      const float value = fabsf(work[row * kDim + column] / sh.next_smoothing[row]);
       maximum = value > maximum ? value : maximum;
     }
     a.next_scales[vb + column] = maximum;
@@ -272,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
     for (int row4 = 0; row4 < kDim; row4 += 4) {
       uint32_t packed = 0;
       for (int i = 0; i < 4; ++i) {
-        const float smoothed = residual_cell(sh, row4 + i, column, bs) / sh.next_smoothing[row4 + i];
+        const float smoothed = work[(row4 + i) * kDim + column] / sh.next_smoothing[row4 + i];
         float q = maximum == 0.0f ? 0.0f : smoothed / maximum * 127.0f;
         q += q >= 0.0f ? 0.5f : -0.5f;
         q = q > 127.0f ? 127.0f : q;
@@ -285,8 +323,8 @@ __global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
 
   // ---- new compensators, cleared window, position ----------------------------
   for (int i = t; i < kDim * kRank; i += kThreads) {
-    a.next_comp_keys[vb * kRank + i] = static_cast<uint16_t>(float_to_half_bits(sh.nk[i]));
-    a.next_comp_values[vb * kRank + i] = static_cast<uint16_t>(float_to_half_bits(sh.nv[i]));
+    a.next_comp_keys[vb * kRank + i] = sh.nk[i];
+    a.next_comp_values[vb * kRank + i] = sh.nv[i];
   }
   for (int i = t; i < kWindow * kDim / 2; i += kThreads) {
     reinterpret_cast<uint32_t*>(a.record_keys + rb * kDim)[i] = 0u;
