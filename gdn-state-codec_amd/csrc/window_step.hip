@@ -174,6 +174,9 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
   if constexpr (kCompensated) {
     comp_key = *reinterpret_cast<const uint4*>(a.comp_keys + (vector_base + k0) * kRank);
   }
+  // Lane j < p holds gate j (one load, issued before the codes so that phase 1
+  // does not wait for them); the other lanes hold 1.0.
+  const float gate_lane = lane < static_cast<int>(p) ? a.record_decay[record_base + lane] : 1.0f;
   // Lane (c, r) = (lane & 7, lane >> 3) reads bytes 16c..16c+15 of rows r + 8j.
   const int8_t* codes = a.residual + static_cast<uint64_t>(state) * kTile;
   const int chunk = lane & 7;
@@ -183,6 +186,10 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
   for (int j = 0; j < 16; ++j) {
     row[j] = stream_load(reinterpret_cast<const uint4*>(codes + (row8 + 8 * j) * kDim + 16 * chunk));
   }
+  // Every load is issued before any phase-1 arithmetic: without this barrier
+  // the scheduler hoists phase-1 math, with its waits for the small operands,
+  // above the code loads, and the 16 KiB stream starts a round trip late.
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- phase 1: vectors, update, compensator and record projections --------
   float read0, read1, out0, out1, write0, write1, query0, query1;
@@ -212,13 +219,15 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
   *reinterpret_cast<float2*>(&weights[wave][1][k0]) = make_float2(sm.x * out0, sm.y * out1);
   const float update = wave_sum(write0 * query0 + write1 * query1);
 
-  // Gate products: suffix_j = prod_{i > j} gate_i over the p stored records.
+  // Gate products: suffix_j = prod_{i > j} gate_i over the p stored records,
+  // in descending i; the 1.0 of lanes j >= p leaves every product unchanged.
   float boundary_suffix = 1.0f;
   float suffix[kWindow];
 #pragma unroll
   for (int j = kWindow - 1; j >= 0; --j) {
     suffix[j] = boundary_suffix;
-    if (j < static_cast<int>(p)) boundary_suffix *= a.record_decay[record_base + j];
+    boundary_suffix *= __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gate_lane), j));
   }
 
   // Record projections key_j . read and key_j . (q*g): 32 partials, one
