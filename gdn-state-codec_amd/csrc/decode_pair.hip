@@ -85,22 +85,25 @@ struct StepVectors {
   uint32_t record_key_bits;  // the record key this lane stores (rows 2*lane..+1)
 };
 
-__device__ __forceinline__ StepVectors bf16_vectors(const uint16_t* keys,
-                                                    const uint16_t* queries,
-                                                    const float* log_decay,
-                                                    const uint16_t* beta,
-                                                    uint32_t state, int lane) {
+// The raw words one lane reads for a step's vectors (rows 2*lane, 2*lane+1),
+// without arithmetic, so a kernel can issue them ahead of its bulk loads.
+struct VectorWords {
+  float decay;     // log decay (bf16 chain) or linear decay (fp16 chain)
+  uint32_t beta;   // bf16 bits; 0 when the chain has no beta
+  uint32_t key;    // bf16 keys (bf16 chain) or fp16 write keys (fp16 chain)
+  uint32_t read;   // fp16 reads (fp16 chain)
+  uint32_t query;
+};
+
+__device__ __forceinline__ StepVectors bf16_vectors(const VectorWords& w) {
   StepVectors v;
-  v.gate = decay_gate(log_decay[state]);
-  const float b = beta != nullptr ? bf16_to_float(beta[state]) : 0.0f;
-  const uint64_t head = static_cast<uint64_t>(state >> 1) * kDim + 2 * lane;
-  const uint32_t kw = *reinterpret_cast<const uint32_t*>(keys + head);
-  const uint32_t qw = *reinterpret_cast<const uint32_t*>(queries + head);
+  v.gate = decay_gate(w.decay);
+  const float b = bf16_to_float(static_cast<uint16_t>(w.beta));
   uint32_t bits = 0;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const float key = bf16_to_float((kw >> (16 * e)) & 0xFFFFu);
-    v.query_raw[e] = bf16_to_float((qw >> (16 * e)) & 0xFFFFu);
+    const float key = bf16_to_float((w.key >> (16 * e)) & 0xFFFFu);
+    v.query_raw[e] = bf16_to_float((w.query >> (16 * e)) & 0xFFFFu);
     v.query[e] = kQueryScale * v.query_raw[e];
     v.read[e] = v.gate * key;
     v.write[e] = b * key;
@@ -110,37 +113,25 @@ __device__ __forceinline__ StepVectors bf16_vectors(const uint16_t* keys,
   return v;
 }
 
-__device__ __forceinline__ StepVectors f16_vectors(const uint16_t* write_keys,
-                                                   const uint16_t* reads,
-                                                   const uint16_t* queries,
-                                                   const float* decay,
-                                                   uint32_t state, int lane) {
+__device__ __forceinline__ StepVectors f16_vectors(const VectorWords& w) {
   StepVectors v;
-  v.gate = decay[state];
-  const uint64_t base = static_cast<uint64_t>(state) * kDim + 2 * lane;
-  const uint32_t ww = write_keys != nullptr ? *reinterpret_cast<const uint32_t*>(write_keys + base) : 0u;
-  const uint32_t rw = *reinterpret_cast<const uint32_t*>(reads + base);
-  const uint32_t qw = *reinterpret_cast<const uint32_t*>(queries + base);
+  v.gate = w.decay;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    v.write[e] = half_bits_to_float((ww >> (16 * e)) & 0xFFFFu);
-    v.read[e] = half_bits_to_float((rw >> (16 * e)) & 0xFFFFu);
-    v.query[e] = half_bits_to_float((qw >> (16 * e)) & 0xFFFFu);
+    v.write[e] = half_bits_to_float((w.key >> (16 * e)) & 0xFFFFu);
+    v.read[e] = half_bits_to_float((w.read >> (16 * e)) & 0xFFFFu);
+    v.query[e] = half_bits_to_float((w.query >> (16 * e)) & 0xFFFFu);
     v.query_raw[e] = v.query[e];
   }
-  v.record_key_bits = ww;
+  v.record_key_bits = w.key;
   return v;
 }
 
 // prepare: pair0 = r*s and pair1 = y*s in the reference's expression order:
 // bf16 ((g*k)*s, ((query_scale*g)*q)*s; encoded_projection.cpp:390-396),
 // fp16 (r*s, (q*g)*s; :265-270).
-__device__ __forceinline__ void prepare_pairs(const StepVectors& v, bool bf16,
-                                              const float* smoothing,
-                                              uint32_t state, int lane,
+__device__ __forceinline__ void prepare_pairs(const StepVectors& v, bool bf16, float2 sm,
                                               float (&pair)[2][2]) {
-  const float2 sm = *reinterpret_cast<const float2*>(
-      smoothing + static_cast<uint64_t>(state) * kDim + 2 * lane);
   const float s[2] = {sm.x, sm.y};
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
@@ -208,7 +199,8 @@ struct FinishShared {
 // in flight during the key staging and the sequential sums.
 __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& sh,
                              const StepVectors& v, uint32_t state, uint32_t p,
-                             int lane, const int32_t (&P)[2][4], const float (&ds)[4]) {
+                             int lane, const int32_t (&P)[2][4], const float (&ds)[4],
+                             float gate_lane) {
   const uint64_t vector_base = static_cast<uint64_t>(state) * kDim;
   const uint64_t record_base = static_cast<uint64_t>(state) * kWindow;
   const int column0 = 2 * lane;
@@ -285,12 +277,15 @@ __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& 
   }
   wave_lds_sync();
   const float update = sh.sums[0];
+  // Gate products in descending record order; the 1.0 of lanes j >= p
+  // leaves every product unchanged.
   float suffix[kWindow];
   float boundary_suffix = 1.0f;
 #pragma unroll
   for (int j = kWindow - 1; j >= 0; --j) {
     suffix[j] = boundary_suffix;
-    if (j < static_cast<int>(p)) boundary_suffix *= a.record_decay[record_base + j];
+    boundary_suffix *= __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gate_lane), j));
   }
   const float value_scale[2] = {scale.x, scale.y};
   const uint32_t comp_words[4] = {cv.x, cv.y, cv.z, cv.w};
@@ -356,10 +351,46 @@ struct VectorArgs {
   bool bf16;
 };
 
+__device__ __forceinline__ VectorWords load_vector_words(const VectorArgs& in, uint32_t state,
+                                                         int lane) {
+  VectorWords w{};
+  w.decay = in.decay[state];
+  if (in.bf16) {
+    w.beta = in.beta != nullptr ? in.beta[state] : 0u;
+    const uint64_t head = static_cast<uint64_t>(state >> 1) * kDim + 2 * lane;
+    w.key = *reinterpret_cast<const uint32_t*>(in.keys + head);
+    w.query = *reinterpret_cast<const uint32_t*>(in.queries + head);
+  } else {
+    const uint64_t base = static_cast<uint64_t>(state) * kDim + 2 * lane;
+    w.key = in.keys != nullptr ? *reinterpret_cast<const uint32_t*>(in.keys + base) : 0u;
+    w.read = *reinterpret_cast<const uint32_t*>(in.reads + base);
+    w.query = *reinterpret_cast<const uint32_t*>(in.queries + base);
+  }
+  return w;
+}
+
+__device__ __forceinline__ StepVectors vectors_of(const VectorWords& w, bool bf16) {
+  return bf16 ? bf16_vectors(w) : f16_vectors(w);
+}
+
 __device__ __forceinline__ StepVectors load_vectors(const VectorArgs& in, uint32_t state,
                                                     int lane) {
-  return in.bf16 ? bf16_vectors(in.keys, in.queries, in.decay, in.beta, state, lane)
-                 : f16_vectors(in.keys, in.reads, in.queries, in.decay, state, lane);
+  return vectors_of(load_vector_words(in, state, lane), in.bf16);
+}
+
+__device__ __forceinline__ float2 load_smoothing(const float* smoothing, uint32_t state,
+                                                 int lane) {
+  return *reinterpret_cast<const float2*>(smoothing + static_cast<uint64_t>(state) * kDim +
+                                          2 * lane);
+}
+
+// Lane j < p holds record gate j, the other lanes 1.0 (the finish's suffix
+// products read it back by readlane).
+__device__ __forceinline__ float load_gate_lane(const FinishArgs& a, uint32_t state, uint32_t p,
+                                                int lane) {
+  return lane < static_cast<int>(p)
+             ? a.record_decay[static_cast<uint64_t>(state) * kWindow + lane]
+             : 1.0f;
 }
 
 __global__ __launch_bounds__(kThreads) void prepare_pair_kernel(
@@ -371,7 +402,7 @@ __global__ __launch_bounds__(kThreads) void prepare_pair_kernel(
   if (state >= in.states) return;
   const StepVectors v = load_vectors(in, state, lane);
   float pair[2][2];
-  prepare_pairs(v, in.bf16, smoothing, state, lane, pair);
+  prepare_pairs(v, in.bf16, load_smoothing(smoothing, state, lane), pair);
   int high[2][2], low[2][2];
   float scale[4];
   split_pair(pair, high, low, scale);
@@ -477,6 +508,7 @@ __global__ __launch_bounds__(kThreads) void finish_pair_kernel(
   if (state >= in.states) return;
   const uint32_t p = fa.positions[static_cast<uint64_t>(state) * kPositionStride];
   if (p >= kWindow) return;
+  const float gate_lane = load_gate_lane(fa, state, p, lane);
   const StepVectors v = load_vectors(in, state, lane);
   int32_t P[2][4];
 #pragma unroll
@@ -487,7 +519,7 @@ __global__ __launch_bounds__(kThreads) void finish_pair_kernel(
   }
   const float4 d = *reinterpret_cast<const float4*>(dynamic_scale + static_cast<uint64_t>(state) * kPositionStride);
   const float ds[4] = {d.x, d.y, d.z, d.w};
-  finish_state(fa, shared[wave], v, state, p, lane, P, ds);
+  finish_state(fa, shared[wave], v, state, p, lane, P, ds, gate_lane);
 }
 
 // Integer analogue of the decode projection's pairwise lane reduction.
@@ -528,8 +560,13 @@ __global__ __launch_bounds__(kThreads) void fused_decode_pair_kernel(
   const uint32_t p = fa.positions[static_cast<uint64_t>(state) * kPositionStride];
   if (p >= kWindow) return;
 
-  // The codes first (the bulk of the traffic), in flight during the prepare.
-  // Lane owns keys 16*kq..+15 of value rows r8 + 8j.
+  // The small operands first, then the codes (the bulk of the traffic):
+  // memory returns in issue order, so the prepare waits only for the small
+  // operands while the codes are in flight.  Lane owns keys 16*kq..+15 of
+  // value rows r8 + 8j.
+  const VectorWords words = load_vector_words(in, state, lane);
+  const float2 sm = load_smoothing(smoothing, state, lane);
+  const float gate_lane = load_gate_lane(fa, state, p, lane);
   const int kq = lane & 7;
   const int r8 = lane >> 3;
   const int8_t* codes = residual + static_cast<uint64_t>(state) * kTile;
@@ -538,10 +575,12 @@ __global__ __launch_bounds__(kThreads) void fused_decode_pair_kernel(
   for (int j = 0; j < 16; ++j) {
     row[j] = stream_load(reinterpret_cast<const uint4*>(codes + (r8 + 8 * j) * kDim + 16 * kq));
   }
+  // Keeps the prepare's arithmetic (and its waits) below the code loads.
+  __builtin_amdgcn_sched_barrier(0);
 
-  const StepVectors v = load_vectors(in, state, lane);
+  const StepVectors v = vectors_of(words, in.bf16);
   float pair[2][2];
-  prepare_pairs(v, in.bf16, smoothing, state, lane, pair);
+  prepare_pairs(v, in.bf16, sm, pair);
   int high[2][2], low[2][2];
   float ds[4];
   split_pair(pair, high, low, ds);
@@ -598,7 +637,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_pair_kernel(
     const int4 w = *reinterpret_cast<const int4*>(&shared[wave].projected[2 * lane + e][0]);
     P[e][0] = w.x; P[e][1] = w.y; P[e][2] = w.z; P[e][3] = w.w;
   }
-  finish_state(fa, shared[wave], v, state, p, lane, P, ds);
+  finish_state(fa, shared[wave], v, state, p, lane, P, ds, gate_lane);
 }
 
 }  // namespace
