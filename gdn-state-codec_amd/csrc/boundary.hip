@@ -110,14 +110,9 @@ __global__ __launch_bounds__(kThreads) void quant_only_refit_kernel(RefitArgs a)
   const uint64_t vector_base = state * kDim;
   const uint64_t record_base = state * kWindow;
 
-  // Gate suffixes in the reference's order (BuildSuffix, :102-111).
-  float suffix[kWindow];
-  float boundary_suffix = 1.0f;
+  float gates[kWindow];
 #pragma unroll
-  for (int j = kWindow - 1; j >= 0; --j) {
-    suffix[j] = boundary_suffix;
-    boundary_suffix *= a.record_decay[record_base + j];
-  }
+  for (int j = 0; j < kWindow; ++j) gates[j] = a.record_decay[record_base + j];
   const int k0 = 2 * lane;
   const int column0 = wave * kColumnsPerWave;
   const int8_t* codes = a.residual + state * kTile;
@@ -127,29 +122,54 @@ __global__ __launch_bounds__(kThreads) void quant_only_refit_kernel(RefitArgs a)
   for (int c = 0; c < kColumnsPerWave; ++c) {
     pair[c] = *reinterpret_cast<const uint16_t*>(codes + (column0 + c) * kDim + k0);
   }
+  // Every other load before any arithmetic that waits on one (memory returns
+  // in issue order): the record corrections of this thread's column (threads
+  // 0..127 take records 0..7 of column t, threads 128..255 records 8..15 of
+  // column t - 128: coalesced 256-byte fp16 rows per record), the column's
+  // scale, this lane's smoothing pair and its two keys of the 16 records.
+  const int own_column = t & (kDim - 1);
+  const int j0 = (t >> 7) * (kWindow / 2);
+  uint16_t correction_bits[kWindow / 2];
+  uint32_t key_words[kWindow];
   if constexpr (!kMerged) {
-    // Threads 0..127 take records 0..7 of column t, threads 128..255 records
-    // 8..15 of column t - 128: coalesced 256-byte fp16 rows per record.
-    const int v = t & (kDim - 1);
-    const int j0 = (t >> 7) * (kWindow / 2);
 #pragma unroll
     for (int jj = 0; jj < kWindow / 2; ++jj) {
-      const int j = j0 + jj;
-      float sfx = suffix[jj];
-      if (j0 != 0) sfx = suffix[jj + kWindow / 2];
-      scaled_corrections[v][j] =
-          half_bits_to_float(a.record_corrections[(record_base + j) * kDim + v]) * sfx;
+      correction_bits[jj] = a.record_corrections[(record_base + j0 + jj) * kDim + own_column];
     }
   }
-  if (t < kDim) factors[t] = a.scales[vector_base + t] * boundary_suffix / 127.0f;
+  const float own_scale = t < kDim ? a.scales[vector_base + t] : 0.0f;
   const float2 sm = *reinterpret_cast<const float2*>(a.smoothing + vector_base + k0);
+  if constexpr (!kMerged) {
+#pragma unroll
+    for (int j = 0; j < kWindow; ++j) {
+      key_words[j] = *reinterpret_cast<const uint32_t*>(a.record_keys + (record_base + j) * kDim + k0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Gate suffixes in the reference's order (BuildSuffix, :102-111).
+  float suffix[kWindow];
+  float boundary_suffix = 1.0f;
+#pragma unroll
+  for (int j = kWindow - 1; j >= 0; --j) {
+    suffix[j] = boundary_suffix;
+    boundary_suffix *= gates[j];
+  }
+  if constexpr (!kMerged) {
+#pragma unroll
+    for (int jj = 0; jj < kWindow / 2; ++jj) {
+      float sfx = suffix[jj];
+      if (j0 != 0) sfx = suffix[jj + kWindow / 2];
+      scaled_corrections[own_column][j0 + jj] = half_bits_to_float(correction_bits[jj]) * sfx;
+    }
+  }
+  if (t < kDim) factors[t] = own_scale * boundary_suffix / 127.0f;
   float key0[kWindow], key1[kWindow];
   if constexpr (!kMerged) {
 #pragma unroll
     for (int j = 0; j < kWindow; ++j) {
-      const uint32_t w = *reinterpret_cast<const uint32_t*>(a.record_keys + (record_base + j) * kDim + k0);
-      key0[j] = half_bits_to_float(w & 0xFFFFu);
-      key1[j] = half_bits_to_float(w >> 16);
+      key0[j] = half_bits_to_float(key_words[j] & 0xFFFFu);
+      key1[j] = half_bits_to_float(key_words[j] >> 16);
     }
   }
   __syncthreads();
