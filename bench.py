@@ -491,33 +491,88 @@ def bench_capsule(steps: int, warmup: int):
     return results
 
 
-def cpu_baseline_capsule(target_seconds: float = 6.0):
-    """Part of the cpu_baseline leg: the C restatement's slot serialize (one
-    thread) on a bounded sample of the bench_capsule batch."""
+def cpu_baseline_capsule(target_seconds: float = 8.0):
+    """Part of the cpu_baseline leg: the C restatement's slot serialize and
+    restore over the whole bench_capsule batch (8192 states, every window
+    position equally often), on one thread and then on every host core this
+    process may use with the states dealt round-robin to the threads.  The one-thread
+    capsules are byte-compared with the GPU's serialize of the same slot."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
     import torch
 
+    from gdn_state_codec import capsule as cap
     from oracle import capsule as C
 
     dev = torch.device("cuda:0")
     slot = capsule_slot(WINDOW_STATES, dev)
+    gpu_blobs = cap.serialize_to_host(slot, cap.CapsuleIdentity(CAPSULE_GEOMETRY, 1, 1))
     names = ("residual", "smoothing", "scales", "compensator_keys", "compensator_values",
              "record_decay", "record_keys", "record_corrections", "positions")
-    sample = 512
     buf = {}
     for n in names:
-        t = getattr(slot, n)[:sample].cpu()
+        t = getattr(slot, n).cpu()
         buf[n] = t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.float16 else (
             t.numpy().view(np.uint32) if n == "positions" else t.numpy())
+    del slot
     identity = C.Identity(CAPSULE_GEOMETRY, 1, 1)
-    done, nbytes, t0 = 0, 0, time.perf_counter()
-    while done < sample and (done < 16 or time.perf_counter() - t0 < target_seconds):
-        nbytes += len(C.slot_serialize(buf, done, 1, identity))
-        done += 1
-    seconds = time.perf_counter() - t0
-    _log(f"cpu capsule serialize (port): {done} capsules in {seconds:.2f} s")
-    return {"capsules_per_s": done / seconds, "capsule_GBps": nbytes / seconds / 1e9,
-            "cores": 1, "kind": "port", "sample": f"{done} capsules of the bench batch"}
+    states = WINDOW_STATES
+    positions = buf["positions"][:, 0].copy()
+
+    def serialize_some(work):
+        # ctypes releases the GIL for the duration of each foreign call.
+        ids, reps = work
+        out = []
+        for _ in range(reps):
+            out = [C.slot_serialize(buf, s, 1, identity) for s in ids]
+        return out
+
+    def restore_some(work):
+        ids, reps = work
+        target = {n: v.copy() for n, v in buf.items()}
+        bad = 0
+        for _ in range(reps):
+            for s in ids:
+                bad += C.slot_restore(blobs[s], target, s, 1, identity, int(positions[s])) != C.OK
+        return bad
+
+    def timed(fn, threads, reps):
+        # Thread i takes states i, i + threads, ...: every thread sees every
+        # window position (capsule size grows with the position).
+        work = [(range(i, states, threads), reps) for i in range(threads)]
+        t0 = time.perf_counter()
+        with ThreadPoolExecutor(threads) as pool:
+            parts = list(pool.map(fn, work))
+        return time.perf_counter() - t0, parts
+
+    ser_1, parts = timed(serialize_some, 1, 1)
+    blobs = parts[0]
+    nbytes = sum(len(b) for b in blobs)
+    identical = blobs == gpu_blobs
+    res_1, bad = timed(restore_some, 1, 1)
+    threads = _cpu_threads()
+    reps = max(1, int(target_seconds / 2 * threads / max(ser_1 + res_1, 1e-6)))
+    ser_n, _ = timed(serialize_some, threads, reps)
+    res_n, bad_n = timed(restore_some, threads, reps)
+    ok = identical and sum(bad) == 0 and sum(bad_n) == 0
+    _log(f"cpu capsule (port): serialize {states} capsules in {ser_1:.2f} s, restore in "
+         f"{res_1:.2f} s on 1 thread; x{reps} in {ser_n:.2f} / {res_n:.2f} s on {threads} "
+         f"threads; GPU capsules byte-identical={identical}")
+
+    def rates(seconds, count):
+        return {"capsules_per_s": count / seconds, "capsule_GBps": nbytes * count / states
+                / seconds / 1e9}
+
+    return {"serialize": {**rates(ser_n, states * reps), "cores": threads,
+                          "single_thread": {**rates(ser_1, states), "cores": 1}},
+            "restore": {**rates(res_n, states * reps), "cores": threads,
+                        "single_thread": {**rates(res_1, states), "cores": 1}},
+            "kind": "port",
+            "sample": f"the whole {states}-capsule bench batch ({nbytes} capsule bytes), "
+                      f"{reps} passes with the states dealt round-robin to {threads} threads; "
+                      f"one pass on 1 thread",
+            "gpu_capsules_byte_identical": bool(ok)}
 
 
 def bench_pool(steps: int, warmup: int):

@@ -350,9 +350,10 @@ uint64_t gdn_oracle_slot_capsule_serialize(
     const uint16_t* record_keys, const uint16_t* record_corrections, uint32_t position,
     const char* geometry, uint64_t generation, uint64_t epoch, uint8_t* out) {
   if (position >= WINDOW) return 0;
-  static int8_t codes[DIM * DIM];
-  static float ck[DIM * RANK], cv[DIM * RANK];
-  static float decay[WINDOW * DIM], key[WINDOW * DIM], correction[WINDOW * DIM];
+  /* Per-thread scratch: callers serialize from several threads at once. */
+  static _Thread_local int8_t codes[DIM * DIM];
+  static _Thread_local float ck[DIM * RANK], cv[DIM * RANK];
+  static _Thread_local float decay[WINDOW * DIM], key[WINDOW * DIM], correction[WINDOW * DIM];
   for (int k = 0; k < DIM; ++k) {
     for (int v = 0; v < DIM; ++v) {
       codes[k * DIM + v] = layout == GDN_ORACLE_LAYOUT_VALUE_KEY ? residual[v * DIM + k]
@@ -387,10 +388,11 @@ int gdn_oracle_slot_capsule_restore(
     float* smoothing, float* scales, uint16_t* comp_keys, uint16_t* comp_values,
     float* record_decay, uint16_t* record_keys, uint16_t* record_corrections,
     uint32_t* position_word) {
-  static int8_t codes[DIM * DIM];
-  static float sm[DIM], sc[DIM], ck[DIM * RANK], cv[DIM * RANK], dense[DIM * DIM];
-  static float decay[WINDOW * DIM], key[WINDOW * DIM], correction[WINDOW * DIM];
-  static uint16_t ck16[DIM * RANK], cv16[DIM * RANK], key16[WINDOW * DIM],
+  /* Per-thread scratch: callers restore from several threads at once. */
+  static _Thread_local int8_t codes[DIM * DIM];
+  static _Thread_local float sm[DIM], sc[DIM], ck[DIM * RANK], cv[DIM * RANK], dense[DIM * DIM];
+  static _Thread_local float decay[WINDOW * DIM], key[WINDOW * DIM], correction[WINDOW * DIM];
+  static _Thread_local uint16_t ck16[DIM * RANK], cv16[DIM * RANK], key16[WINDOW * DIM],
       correction16[WINDOW * DIM];
   uint32_t count = 0;
   const int status = gdn_oracle_capsule_restore(
