@@ -385,6 +385,13 @@ struct PackArgs {
 // column reads of 8 consecutive rows fall in different LDS banks.
 constexpr int kTileStride = kDim + 4;
 
+// Record floats of records 0..14 as float2 pairs, spread over the workgroup:
+// pair u is handled by thread u % 256 in slot u / 256.  A wavefront's 64 pairs
+// are one 128-float vector (decay, key or correction of one record), so every
+// per-vector quantity is wave-uniform.
+constexpr int kRecordPairSlots = ((kWindow - 1) * kRecordFloats / 2 + kThreads - 1) / kThreads;
+static_assert(kRecordFloats / 2 % 64 == 0, "a record is whole wavefronts of pairs");
+
 __device__ __forceinline__ uint32_t header_word(int t, uint32_t position, const Identity& id) {
   switch (t) {
     case 0: return static_cast<uint32_t>(kMagicWord);
@@ -418,23 +425,82 @@ __global__ __launch_bounds__(kThreads) void capsule_pack_kernel(PackArgs a) {
     return;
   }
   uint8_t* out = a.capsules + offset;
+
+  // Every load first: smoothing then scales (one float per thread), the
+  // compensators (two fp16 each), the records as 32-bit words (pair u of the
+  // capsule's record floats: a gate, or two fp16 keys or corrections), then
+  // the codes.
+  const float value = t < kDim ? a.smoothing[static_cast<uint64_t>(s) * kDim + t]
+                               : a.scales[static_cast<uint64_t>(s) * kDim + t - kDim];
+  const uint64_t comp_base = static_cast<uint64_t>(s) * kDim * kRank;
+  const uint32_t keys = reinterpret_cast<const uint32_t*>(a.comp_keys + comp_base)[t];
+  const uint32_t values = reinterpret_cast<const uint32_t*>(a.comp_values + comp_base)[t];
+  const uint64_t record_base = static_cast<uint64_t>(s) * kWindow;
+  const uint32_t record_pairs = kRecordFloats / 2 * position;  // a multiple of 64
+  uint32_t rec[kRecordPairSlots];
+#pragma unroll
+  for (int i = 0; i < kRecordPairSlots; ++i) {
+    const uint32_t u = i * kThreads + t;
+    rec[i] = 0;
+    if (u < record_pairs) {  // uniform over the wavefront, as is the vector
+      const uint32_t j = u / (kRecordFloats / 2), pair = u - j * (kRecordFloats / 2);
+      if (pair < kDim / 2) {
+        rec[i] = __float_as_uint(a.record_decay[record_base + j]);
+      } else if (pair < kDim) {
+        rec[i] = reinterpret_cast<const uint32_t*>(a.record_keys + (record_base + j) * kDim)[pair - kDim / 2];
+      } else {
+        rec[i] = reinterpret_cast<const uint32_t*>(a.record_corrections + (record_base + j) * kDim)[pair - kDim];
+      }
+    }
+  }
+  // Codes: [value][key] rows to transpose (thread = half a row), or
+  // [key][value] words copied as they are.
+  const int8_t* codes = a.residual + static_cast<uint64_t>(s) * kTile;
+  uint4 row_part[4];
+  uint64_t words[8];
+  if (a.layout == kValueKey) {
+    const uint4* src = reinterpret_cast<const uint4*>(codes + (t >> 1) * kDim + (t & 1) * 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) row_part[i] = src[i];
+  } else {
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(codes);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) words[i] = src[i * kThreads + t];
+  }
+  // Keep the stores below from being scheduled between the loads.
+  __builtin_amdgcn_sched_barrier(0);
+
   if (t < static_cast<int>(kHeaderWords)) {
     *reinterpret_cast<uint32_t*>(out + 4 * t) = header_word(t, position, a.identity);
   }
+  *reinterpret_cast<float*>(out + kSmoothingOffset + 4 * t) = value;
+  reinterpret_cast<float2*>(out + kCompKeysOffset)[t] =
+      make_float2(half_bits_to_float(keys & 0xFFFFu), half_bits_to_float(keys >> 16));
+  reinterpret_cast<float2*>(out + kCompValuesOffset)[t] =
+      make_float2(half_bits_to_float(values & 0xFFFFu), half_bits_to_float(values >> 16));
+  // Records 0..p-1: {gate repeated over the keys, key, correction}.
+  float2* records = reinterpret_cast<float2*>(out + kRecordsOffset);
+#pragma unroll
+  for (int i = 0; i < kRecordPairSlots; ++i) {
+    const uint32_t u = i * kThreads + t;
+    if (u < record_pairs) {
+      const bool gate = (u / 64) % 3 == 0;
+      records[u] = gate ? make_float2(__uint_as_float(rec[i]), __uint_as_float(rec[i]))
+                        : make_float2(half_bits_to_float(rec[i] & 0xFFFFu),
+                                      half_bits_to_float(rec[i] >> 16));
+    }
+  }
   // Codes in [key][value] order: 2048 8-byte words, word w = 16 k + v / 8.
-  const int8_t* codes = a.residual + static_cast<uint64_t>(s) * kTile;
   uint64_t* residual_out = reinterpret_cast<uint64_t*>(out + kResidualOffset);
   if (a.layout == kValueKey) {
     const int row = t >> 1, half = t & 1;  // source row = value
-    const uint4* src = reinterpret_cast<const uint4*>(codes + row * kDim + half * 64);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint4 v = src[i];
       uint32_t* dst = reinterpret_cast<uint32_t*>(tile + row * kTileStride + half * 64 + 16 * i);
-      dst[0] = v.x;
-      dst[1] = v.y;
-      dst[2] = v.z;
-      dst[3] = v.w;
+      dst[0] = row_part[i].x;
+      dst[1] = row_part[i].y;
+      dst[2] = row_part[i].z;
+      dst[3] = row_part[i].w;
     }
     __syncthreads();
 #pragma unroll
@@ -449,40 +515,8 @@ __global__ __launch_bounds__(kThreads) void capsule_pack_kernel(PackArgs a) {
       residual_out[w] = word;
     }
   } else {
-    const uint64_t* src = reinterpret_cast<const uint64_t*>(codes);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) residual_out[i * kThreads + t] = src[i * kThreads + t];
-  }
-  // Smoothing then scales: 256 floats, one per thread.
-  {
-    const float value = t < kDim ? a.smoothing[static_cast<uint64_t>(s) * kDim + t]
-                                 : a.scales[static_cast<uint64_t>(s) * kDim + t - kDim];
-    *reinterpret_cast<float*>(out + kSmoothingOffset + 4 * t) = value;
-  }
-  // Compensators [128][4] fp16 -> fp32, two per thread for each.
-  {
-    const uint64_t base = static_cast<uint64_t>(s) * kDim * kRank;
-    const uint32_t keys = reinterpret_cast<const uint32_t*>(a.comp_keys + base)[t];
-    const uint32_t values = reinterpret_cast<const uint32_t*>(a.comp_values + base)[t];
-    reinterpret_cast<float2*>(out + kCompKeysOffset)[t] =
-        make_float2(half_bits_to_float(keys & 0xFFFFu), half_bits_to_float(keys >> 16));
-    reinterpret_cast<float2*>(out + kCompValuesOffset)[t] =
-        make_float2(half_bits_to_float(values & 0xFFFFu), half_bits_to_float(values >> 16));
-  }
-  // Records 0..p-1: {gate repeated over the keys, key, correction}.
-  float* records = reinterpret_cast<float*>(out + kRecordsOffset);
-  const uint64_t record_base = static_cast<uint64_t>(s) * kWindow;
-  for (uint32_t w = t; w < kRecordFloats * position; w += kThreads) {
-    const uint32_t j = w / kRecordFloats, i = w - j * kRecordFloats;
-    float value;
-    if (i < kDim) {
-      value = a.record_decay[record_base + j];
-    } else if (i < 2 * kDim) {
-      value = half_bits_to_float(a.record_keys[(record_base + j) * kDim + i - kDim]);
-    } else {
-      value = half_bits_to_float(a.record_corrections[(record_base + j) * kDim + i - 2 * kDim]);
-    }
-    records[w] = value;
+    for (int i = 0; i < 8; ++i) residual_out[i * kThreads + t] = words[i];
   }
   if (t == 0) a.lengths[s] = static_cast<uint32_t>(bytes);
 }
@@ -520,10 +554,22 @@ __device__ __forceinline__ bool half_exact(float x) {
   return back == __float_as_uint(x);
 }
 
+// Maximum over the wavefront of non-negative float bits, in every lane.
+__device__ __forceinline__ uint32_t wave_max_bits(uint32_t x) {
+  // Row prefixes by DPP row shifts, then rows merged by row broadcasts: lane
+  // 63 ends with the maximum.  A lane whose source is outside the row keeps
+  // its own value (bound_ctrl off, old = x).
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x111, 0xF, 0xF, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x112, 0xF, 0xF, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x114, 0xF, 0xF, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x118, 0xF, 0xF, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x142, 0xA, 0xF, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x143, 0xC, 0xF, false)));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 63));
+}
+
 __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) {
   __shared__ uint32_t header[kHeaderWords];
-  __shared__ float sm[kDim], sc[kDim], ck[kDim * kRank], cv[kDim * kRank];
-  __shared__ float rec[(kWindow - 1) * kRecordFloats];  // records 0..14
   // |max| of smoothing, scales, ck, cv, then (decay, key, correction) of each
   // record, as float bits (non-negative floats order like their bits).
   __shared__ uint32_t maxima[4 + 3 * (kWindow - 1)];
@@ -538,67 +584,75 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
   const uint32_t content = a.lengths[s] - kDigestChars;
   if (t < 2) flags[t] = 0u;
   if (t < 4 + 3 * (kWindow - 1)) maxima[t] = 0u;
-  __syncthreads();
 
-  // Every load the checks need, issued together.  What is present depends
-  // only on the content length; which of it counts is decided below.
+  // Every load the checks and the slot writes need, issued together and held
+  // in registers.  What is present depends only on the content length; which
+  // of it counts is decided below.
   const bool has_header = content >= kResidualOffset;
   const bool has_codes = content >= kSmoothingOffset;
   const bool has_payload = content >= kRecordsOffset;
   const uint32_t whole = has_payload ? (content - kRecordsOffset) / kRecordBytes : 0u;
   const uint32_t loaded = whole < kWindow - 1 ? whole : kWindow - 1;
+  const uint32_t loaded_pairs = kRecordFloats / 2 * loaded;  // a multiple of 64
+  uint32_t header_bits = 0;
   if (has_header && t < static_cast<int>(kHeaderWords)) {
-    header[t] = reinterpret_cast<const uint32_t*>(base)[t];
+    header_bits = reinterpret_cast<const uint32_t*>(base)[t];
   }
   uint64_t codes[8];
-  bool minus128 = false;
 #pragma unroll
   for (int i = 0; i < 8; ++i) codes[i] = 0;
   if (has_codes) {
     const uint64_t* code_words = reinterpret_cast<const uint64_t*>(base + kResidualOffset);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      codes[i] = code_words[i * kThreads + t];
-      minus128 = minus128 || has_byte_0x80(codes[i]);
-    }
+    for (int i = 0; i < 8; ++i) codes[i] = code_words[i * kThreads + t];
   }
+  // Thread t < 128 holds smoothing[t], the others scales[t - 128].
+  float value = 0.0f;
   float2 key_pair = make_float2(0.0f, 0.0f), value_pair = make_float2(0.0f, 0.0f);
-  bool payload_bad = false;
-  const int lane = t & 63;
-  // A wavefront's 64 values of one slot are reduced first, then merged into
-  // the workgroup's slot by one atomic.
-  const auto merge_max = [&](int slot, float magnitude) {
-    const float m = wave_max(magnitude);
-    if (lane == 0) atomicMax(&maxima[slot], __float_as_uint(m));
-  };
+  float2 rec[kRecordPairSlots];
   if (has_payload) {
-    const float value = *reinterpret_cast<const float*>(base + kSmoothingOffset + 4 * t);
-    if (t < kDim) {
-      sm[t] = value;
-      payload_bad = !(isfinite(value) && value > 0.0f);
-    } else {
-      sc[t - kDim] = value;
-      payload_bad = !(isfinite(value) && value >= 0.0f);
-    }
-    merge_max(t < kDim ? 0 : 1, fabsf(value));  // waves 0-1 smoothing, 2-3 scales
+    value = *reinterpret_cast<const float*>(base + kSmoothingOffset + 4 * t);
     key_pair = reinterpret_cast<const float2*>(base + kCompKeysOffset)[t];
     value_pair = reinterpret_cast<const float2*>(base + kCompValuesOffset)[t];
-    ck[2 * t] = key_pair.x;
-    ck[2 * t + 1] = key_pair.y;
-    cv[2 * t] = value_pair.x;
-    cv[2 * t + 1] = value_pair.y;
+  }
+  const float2* record_pairs = reinterpret_cast<const float2*>(base + kRecordsOffset);
+#pragma unroll
+  for (int i = 0; i < kRecordPairSlots; ++i) {
+    const uint32_t u = i * kThreads + t;
+    rec[i] = u < loaded_pairs ? record_pairs[u] : make_float2(0.0f, 0.0f);
+  }
+  // Keep the checks below from being scheduled between the loads.
+  __builtin_amdgcn_sched_barrier(0);
+
+  if (has_header && t < static_cast<int>(kHeaderWords)) header[t] = header_bits;
+  bool minus128 = false;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) minus128 = minus128 || has_byte_0x80(codes[i]);
+  bool payload_bad = false;
+  const int lane = t & 63;
+  __syncthreads();  // flags and maxima are clear
+  // A wavefront's 64 magnitudes of one vector are reduced first, then merged
+  // into the workgroup's slot by one atomic.
+  const auto merge_max = [&](int slot, float magnitude) {
+    const uint32_t m = wave_max_bits(__float_as_uint(magnitude));
+    if (lane == 0) atomicMax(&maxima[slot], m);
+  };
+  if (has_payload) {
+    payload_bad = t < kDim ? !(isfinite(value) && value > 0.0f) : !(isfinite(value) && value >= 0.0f);
+    merge_max(t < kDim ? 0 : 1, fabsf(value));  // waves 0-1 smoothing, 2-3 scales
     payload_bad = payload_bad || !isfinite(key_pair.x) || !isfinite(key_pair.y) ||
                   !isfinite(value_pair.x) || !isfinite(value_pair.y);
     merge_max(2, fmaxf(fabsf(key_pair.x), fabsf(key_pair.y)));
     merge_max(3, fmaxf(fabsf(value_pair.x), fabsf(value_pair.y)));
-    // w = i * 256 + t: a wavefront's 64 values lie in one 128-value vector.
-    const float* src = reinterpret_cast<const float*>(base + kRecordsOffset);
-    for (uint32_t w = t; w < kRecordFloats * loaded; w += kThreads) {
-      const float value = src[w];
-      rec[w] = value;
-      const uint32_t j = w / kRecordFloats;
-      if (!isfinite(value)) atomicOr(&flags[1], 1u << j);
-      merge_max(4 + static_cast<int>(w / kDim), fabsf(value));
+#pragma unroll
+    for (int i = 0; i < kRecordPairSlots; ++i) {
+      const uint32_t u = i * kThreads + t;
+      if (u < loaded_pairs) {  // uniform over the wavefront
+        if (!isfinite(rec[i].x) || !isfinite(rec[i].y)) {
+          atomicOr(&flags[1], 1u << (u / (kRecordFloats / 2)));
+        }
+        merge_max(4 + static_cast<int>(u / 64), fmaxf(fabsf(rec[i].x), fabsf(rec[i].y)));
+      }
     }
   }
   if (minus128 || payload_bad) {
@@ -662,8 +716,9 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
   // reference's fp32 evaluation forms after s*code is at most
   // B_p (1 + 2^-24)^40 in magnitude, so B_p and max|s| * 127 below
   // FLT_MAX (1 - 2^-10) prove the state finite.  Otherwise it is evaluated
-  // exactly, in its own order: ((s*code)/127)*scale, + ck.cv over the rank,
-  // then decay*x + key*corr per record (the build disables contraction).
+  // exactly, in its own order, from the capsule's bytes: ((s*code)/127)*scale,
+  // + ck.cv over the rank, then decay*x + key*corr per record (the build
+  // disables contraction).
   const auto mx = [&](int slot) { return static_cast<double>(__uint_as_float(maxima[slot])); };
   double bound = mx(0) * mx(1) + 4.0 * mx(2) * mx(3);
   for (uint32_t j = 0; j < count; ++j) {
@@ -672,26 +727,27 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
   const double limit = static_cast<double>(FLT_MAX) * (1.0 - 1.0 / 1024.0);
   bool bad = false;
   if (!(bound < limit && mx(0) * 127.0 < limit)) {
+    const float* sm = reinterpret_cast<const float*>(base + kSmoothingOffset);
+    const float* sc = reinterpret_cast<const float*>(base + kScalesOffset);
+    const float* ck = reinterpret_cast<const float*>(base + kCompKeysOffset);
+    const float* cv = reinterpret_cast<const float*>(base + kCompValuesOffset);
+    const float* records = reinterpret_cast<const float*>(base + kRecordsOffset);
+    const int8_t* code_bytes = reinterpret_cast<const int8_t*>(base + kResidualOffset);
+    // A rare path: one element at a time, in few registers.  Element b of
+    // this thread's code word w is (key k, value v).
+#pragma unroll 1
+    for (int e = 0; e < 64; ++e) {
+      const int w = (e >> 3) * kThreads + t, b = e & 7;
+      const int k = w >> 4, v = (w & 15) * 8 + b;
+      const float code = static_cast<float>(code_bytes[8 * w + b]);
+      float x = sm[k] * code / 127.0f * sc[v];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int w = i * kThreads + t;
-      const int k = w >> 4, v0 = (w & 15) * 8;
-      float x[8];
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const float code = static_cast<float>(static_cast<int8_t>(codes[i] >> (8 * b)));
-        x[b] = sm[k] * code / 127.0f * sc[v0 + b];
-#pragma unroll
-        for (int r = 0; r < kRank; ++r) x[b] += ck[k * kRank + r] * cv[(v0 + b) * kRank + r];
-      }
+      for (int r = 0; r < kRank; ++r) x += ck[k * kRank + r] * cv[v * kRank + r];
       for (uint32_t j = 0; j < count; ++j) {
-        const float* r = rec + j * kRecordFloats;
-        const float decay = r[k], key = r[kDim + k];
-#pragma unroll
-        for (int b = 0; b < 8; ++b) x[b] = decay * x[b] + key * r[2 * kDim + v0 + b];
+        const float* r = records + j * kRecordFloats;
+        x = r[k] * x + r[kDim + k] * r[2 * kDim + v];
       }
-#pragma unroll
-      for (int b = 0; b < 8; ++b) bad = bad || !isfinite(x[b]);
+      bad = bad || !isfinite(x);
     }
     if (__syncthreads_or(bad)) {
       if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_STATE_NONFINITE;
@@ -699,13 +755,21 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
     }
   }
   // The slot's format: one gate per record, fp16 compensators and records.
+  const uint32_t count_pairs = kRecordFloats / 2 * count;
   bad = !half_exact(key_pair.x) || !half_exact(key_pair.y) || !half_exact(value_pair.x) ||
         !half_exact(value_pair.y);
-  for (uint32_t w = t; w < kRecordFloats * count; w += kThreads) {
-    const uint32_t j = w / kRecordFloats, i = w - j * kRecordFloats;
-    const float value = rec[w];
-    bad = bad || (i < kDim ? __float_as_uint(value) != __float_as_uint(rec[j * kRecordFloats])
-                           : !half_exact(value));
+#pragma unroll
+  for (int i = 0; i < kRecordPairSlots; ++i) {
+    const uint32_t u = i * kThreads + t;
+    if (u < count_pairs) {  // uniform over the wavefront, as is the vector
+      if ((u / 64) % 3 == 0) {  // a decay vector: every value equals its first (lane 0's)
+        const uint32_t first =
+            static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(rec[i].x)), 0));
+        bad = bad || __float_as_uint(rec[i].x) != first || __float_as_uint(rec[i].y) != first;
+      } else {
+        bad = bad || !half_exact(rec[i].x) || !half_exact(rec[i].y);
+      }
+    }
   }
   if (__syncthreads_or(bad)) {
     if (t == 0) a.status[s] = GDN_STATE_CODEC_CAPSULE_DEVICE_FORMAT;
@@ -741,9 +805,9 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
     for (int i = 0; i < 8; ++i) out[i * kThreads + t] = codes[i];
   }
   if (t < kDim) {
-    a.smoothing[static_cast<uint64_t>(s) * kDim + t] = sm[t];
+    a.smoothing[static_cast<uint64_t>(s) * kDim + t] = value;
   } else {
-    a.scales[static_cast<uint64_t>(s) * kDim + t - kDim] = sc[t - kDim];
+    a.scales[static_cast<uint64_t>(s) * kDim + t - kDim] = value;
   }
   {
     const uint64_t comp_base = static_cast<uint64_t>(s) * kDim * kRank;
@@ -752,19 +816,24 @@ __global__ __launch_bounds__(kThreads) void capsule_unpack_kernel(UnpackArgs a) 
     reinterpret_cast<uint32_t*>(a.comp_values + comp_base)[t] =
         float_to_half_bits(value_pair.x) | (float_to_half_bits(value_pair.y) << 16);
   }
+  // Records 0..p-1 from the registers: the gate once, keys and corrections
+  // two fp16 values per 32-bit store.
   const uint64_t record_base = static_cast<uint64_t>(s) * kWindow;
-  if (static_cast<uint32_t>(t) < count) {
-    a.record_decay[record_base + t] = rec[t * kRecordFloats];
-  }
-  // Keys and corrections of records 0..p-1, two fp16 values per 32-bit store.
-  for (uint32_t w = t; w < kDim * count; w += kThreads) {
-    const uint32_t j = w / kDim, pair = w - j * kDim;  // pair < 64: keys, else corrections
-    const float* r = rec + j * kRecordFloats + kDim;  // key[0..127], correction[0..127]
-    const uint32_t bits = float_to_half_bits(r[2 * pair]) | (float_to_half_bits(r[2 * pair + 1]) << 16);
-    uint16_t* dst = pair < kDim / 2 ? a.record_keys + (record_base + j) * kDim + 2 * pair
+#pragma unroll
+  for (int i = 0; i < kRecordPairSlots; ++i) {
+    const uint32_t u = i * kThreads + t;
+    if (u < count_pairs) {
+      const uint32_t j = u / (kRecordFloats / 2), pair = u - j * (kRecordFloats / 2);
+      if (pair < kDim / 2) {
+        if (pair == 0) a.record_decay[record_base + j] = rec[i].x;
+      } else {
+        const uint32_t bits = float_to_half_bits(rec[i].x) | (float_to_half_bits(rec[i].y) << 16);
+        uint16_t* dst = pair < kDim ? a.record_keys + (record_base + j) * kDim + 2 * (pair - kDim / 2)
                                     : a.record_corrections + (record_base + j) * kDim +
-                                          2 * (pair - kDim / 2);
-    *reinterpret_cast<uint32_t*>(dst) = bits;
+                                          2 * (pair - kDim);
+        *reinterpret_cast<uint32_t*>(dst) = bits;
+      }
+    }
   }
   if (t == 0) {
     a.positions[static_cast<uint64_t>(s) * kPositionStride] = count;
