@@ -34,6 +34,37 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kPairColumns = 16;  // quantized / projected row width
 
+// Cross-lane steps by DPP on the VALU rather than ds_bpermute through the
+// LDS unit.  dpp<ctrl, row_mask>(x): a lane whose source is outside its row,
+// or whose row is masked off, keeps its own x.
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ int dpp(int x) {
+  return __builtin_amdgcn_update_dpp(x, x, kCtrl, kRowMask, 0xF, false);
+}
+constexpr int kQuadSwap1 = 0xB1;    // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kQuadSwap2 = 0x4E;    // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kQuadReverse = 0x1B;  // quad_perm [3,2,1,0]: lane ^ 3
+constexpr int kHalfMirror = 0x141;  // row_half_mirror: lane 7 - lane within 8
+
+// Value of lane ^ 4: (lane ^ 3) then 7 - that, within each group of 8.
+__device__ __forceinline__ int from_lane_xor4(int x) {
+  return dpp<kHalfMirror>(dpp<kQuadReverse>(x));
+}
+
+// Maximum over the wavefront, in every lane (fmaxf, so the order of the
+// comparisons cannot change the result): row prefixes by row_shr 1, 2, 4, 8,
+// rows merged by row_bcast 15 and 31, then lane 63 read back.
+__device__ __forceinline__ float wave_max_dpp(float x) {
+  const auto step = [](float v, int other) { return fmaxf(v, __int_as_float(other)); };
+  x = step(x, dpp<0x111>(__float_as_int(x)));
+  x = step(x, dpp<0x112>(__float_as_int(x)));
+  x = step(x, dpp<0x114>(__float_as_int(x)));
+  x = step(x, dpp<0x118>(__float_as_int(x)));
+  x = step(x, dpp<0x142, 0xA>(__float_as_int(x)));
+  x = step(x, dpp<0x143, 0xC>(__float_as_int(x)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
 // Vector quantizer rounding of the reference: add +-0.5, clamp, truncate.
 __device__ __forceinline__ int pair_round(float value) {
   float r = value + (value >= 0.0f ? 0.5f : -0.5f);
@@ -50,7 +81,7 @@ __device__ __forceinline__ void split_pair(const float (&pair)[2][2],
                                            float (&scale)[4]) {
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
-    const float m = wave_max(fmaxf(fabsf(pair[c][0]), fabsf(pair[c][1])));
+    const float m = wave_max_dpp(fmaxf(fabsf(pair[c][0]), fabsf(pair[c][1])));
     scale[c] = m > 1.0e-20f ? m / 127.0f : 1.0f;
   }
   float residual_max[2];
@@ -63,7 +94,7 @@ __device__ __forceinline__ void split_pair(const float (&pair)[2][2],
       const float residual = pair[c][e] - static_cast<float>(high[c][e]) * scale[c];
       m = fmaxf(m, fabsf(residual));
     }
-    residual_max[c] = wave_max(m);
+    residual_max[c] = wave_max_dpp(m);
   }
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
@@ -176,15 +207,20 @@ struct FinishArgs {
   bool bf16;
 };
 
+// Basis rows are padded to 272 bytes: in the sums every lane reads its own
+// row at the same column, and a 256-byte stride would put all of them in one
+// LDS bank; at 272 bytes any 16 consecutive lanes fall in distinct banks.
+constexpr int kBasisStride = kDim + 8;
+
 // LDS a wavefront needs for the finish: the three vectors, the compensator
-// and record keys widened to fp32 (rows 0..3 and 4..4+p-1), and the 41 sums.
+// and record keys (rows 0..3 and 4..4+p-1), and the 41 sums.
 struct FinishShared {
   float read[kDim];
   float query[kDim];
   float write[kDim];
   union {
     // Compensator then record keys as fp16 bits (exact; widened when read).
-    uint16_t basis[kRank + kWindow][kDim];
+    uint16_t basis[kRank + kWindow][kBasisStride];
     // Fused kernel only: the projections by value, read back before the keys
     // are staged (a wavefront's LDS accesses complete in program order).
     int32_t projected[kDim][4];
@@ -266,12 +302,13 @@ __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& 
     if (lane == 0) {
 #pragma unroll 16
       for (int row = 0; row < kDim; ++row) acc += sh.write[row] * x[row];
-    } else if (gated) {
-#pragma unroll 16
-      for (int row = 0; row < kDim; ++row) acc += half_bits_to_float(basis[row]) * x[row] * v.gate;
     } else {
+      // One loop for the read and the output sides (divergent loops would
+      // run one after the other): the read side multiplies by 1.0, which
+      // leaves every product unchanged.
+      const float g = gated ? v.gate : 1.0f;
 #pragma unroll 16
-      for (int row = 0; row < kDim; ++row) acc += half_bits_to_float(basis[row]) * x[row];
+      for (int row = 0; row < kDim; ++row) acc += half_bits_to_float(basis[row]) * x[row] * g;
     }
     sh.sums[lane] = acc;
   }
@@ -424,7 +461,7 @@ __global__ __launch_bounds__(kThreads) void prepare_vector_kernel(
     x[e] = half_bits_to_float(input[row * kPairColumns]) * axis_scale[row];
     m = fmaxf(m, fabsf(x[e]));
   }
-  m = wave_max(m);
+  m = wave_max_dpp(m);
   const float scale = m > 1.0e-20f ? m / 127.0f : 1.0f;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
@@ -529,21 +566,21 @@ __device__ __forceinline__ void reduce16_over_8_lanes_int(int32_t (&p)[16], int 
     const bool up = (lane & 4) != 0;
     const int32_t send = up ? p[i] : p[i + 8];
     const int32_t keep = up ? p[i + 8] : p[i];
-    p[i] = keep + __shfl_xor(send, 4);
+    p[i] = keep + from_lane_xor4(send);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const bool up = (lane & 2) != 0;
     const int32_t send = up ? p[i] : p[i + 4];
     const int32_t keep = up ? p[i + 4] : p[i];
-    p[i] = keep + __shfl_xor(send, 2);
+    p[i] = keep + dpp<kQuadSwap2>(send);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const bool up = (lane & 1) != 0;
     const int32_t send = up ? p[i] : p[i + 2];
     const int32_t keep = up ? p[i + 2] : p[i];
-    p[i] = keep + __shfl_xor(send, 1);
+    p[i] = keep + dpp<kQuadSwap1>(send);
   }
 }
 
