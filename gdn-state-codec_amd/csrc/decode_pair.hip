@@ -218,21 +218,60 @@ struct FinishShared {
   float read[kDim];
   float query[kDim];
   float write[kDim];
-  union {
-    // Compensator then record keys as fp16 bits (exact; widened when read).
-    uint16_t basis[kRank + kWindow][kBasisStride];
-    // Fused kernel only: the projections by value, read back before the keys
-    // are staged (a wavefront's LDS accesses complete in program order).
-    int32_t projected[kDim][4];
-  };
+  // Compensator then record keys as fp16 bits (exact; widened when read).
+  uint16_t basis[kRank + kWindow][kBasisStride];
   float sums[1 + 2 * kRank + 2 * kWindow];
 };
+
+// The key words of one lane: its two keys' four compensator halves and, for
+// records j < p, its two record-key halves.
+struct KeyWords {
+  uint4 comp;
+  uint32_t record[kWindow];
+};
+
+__device__ __forceinline__ KeyWords load_key_words(const FinishArgs& a, uint32_t state,
+                                                   uint32_t p, int lane) {
+  const uint64_t vector_base = static_cast<uint64_t>(state) * kDim;
+  const uint64_t record_base = static_cast<uint64_t>(state) * kWindow;
+  KeyWords k;
+  // comp_keys [state][key][4]: this lane's two keys are 8 contiguous halves.
+  k.comp = *reinterpret_cast<const uint4*>(a.comp_keys + (vector_base + 2 * lane) * kRank);
+#pragma unroll
+  for (int j = 0; j < kWindow; ++j) {
+    k.record[j] = j < static_cast<int>(p)
+        ? *reinterpret_cast<const uint32_t*>(a.record_keys + (record_base + j) * kDim + 2 * lane)
+        : 0u;
+  }
+  return k;
+}
+
+// Basis rows 0..3 (compensator keys, transposed to [rank][key]) and
+// 4..4+p-1 (record keys).
+__device__ __forceinline__ void stage_keys(FinishShared& sh, const KeyWords& k, uint32_t p,
+                                           int lane) {
+  const uint32_t words[4] = {k.comp.x, k.comp.y, k.comp.z, k.comp.w};
+#pragma unroll
+  for (int r = 0; r < kRank; ++r) {
+    const uint32_t k0 = (words[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
+    const uint32_t k1 = (words[2 + (r >> 1)] >> (16 * (r & 1))) & 0xFFFFu;
+    *reinterpret_cast<uint32_t*>(&sh.basis[r][2 * lane]) = k0 | (k1 << 16);
+  }
+#pragma unroll
+  for (int j = 0; j < kWindow; ++j) {
+    if (j < static_cast<int>(p)) {
+      *reinterpret_cast<uint32_t*>(&sh.basis[kRank + j][2 * lane]) = k.record[j];
+    }
+  }
+}
 
 // Finishes one state at position p < 16 for this lane's two values
 // 2*lane, 2*lane+1, given the int32 projections P[e][c] (c = hi0, lo0, hi1,
 // lo1) and the dynamic scales.  The per-value operands (scales, compensator
 // values, values and the p record corrections) are loaded first, so they are
 // in flight during the key staging and the sequential sums.
+// kKeysStaged: the caller has already written the basis rows (stage_keys).
+template <bool kKeysStaged>
 __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& sh,
                              const StepVectors& v, uint32_t state, uint32_t p,
                              int lane, const int32_t (&P)[2][4], const float (&ds)[4],
@@ -256,24 +295,7 @@ __device__ __forceinline__ void finish_state(const FinishArgs& a, FinishShared& 
     sh.query[2 * lane + e] = v.query[e];
     sh.write[2 * lane + e] = v.write[e];
   }
-  {
-    // comp_keys [state][key][4]: this lane's two keys are 8 contiguous halves.
-    const uint4 ck = *reinterpret_cast<const uint4*>(a.comp_keys + (vector_base + 2 * lane) * kRank);
-    const uint32_t words[4] = {ck.x, ck.y, ck.z, ck.w};
-#pragma unroll
-    for (int r = 0; r < kRank; ++r) {
-      const uint32_t k0 = (words[r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
-      const uint32_t k1 = (words[2 + (r >> 1)] >> (16 * (r & 1))) & 0xFFFFu;
-      *reinterpret_cast<uint32_t*>(&sh.basis[r][2 * lane]) = k0 | (k1 << 16);
-    }
-#pragma unroll
-    for (int j = 0; j < kWindow; ++j) {
-      if (j < static_cast<int>(p)) {
-        *reinterpret_cast<uint32_t*>(&sh.basis[kRank + j][2 * lane]) =
-            *reinterpret_cast<const uint32_t*>(a.record_keys + (record_base + j) * kDim + 2 * lane);
-      }
-    }
-  }
+  if constexpr (!kKeysStaged) stage_keys(sh, load_key_words(a, state, p, lane), p, lane);
   wave_lds_sync();
   // Sequential sums in row order, one per lane: 0 = update, 1..4 = old read
   // projections, 5..8 = old output projections, 9.. = record read projections
@@ -556,7 +578,7 @@ __global__ __launch_bounds__(kThreads) void finish_pair_kernel(
   }
   const float4 d = *reinterpret_cast<const float4*>(dynamic_scale + static_cast<uint64_t>(state) * kPositionStride);
   const float ds[4] = {d.x, d.y, d.z, d.w};
-  finish_state(fa, shared[wave], v, state, p, lane, P, ds, gate_lane);
+  finish_state<false>(fa, shared[wave], v, state, p, lane, P, ds, gate_lane);
 }
 
 // Integer analogue of the decode projection's pairwise lane reduction.
@@ -590,6 +612,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_pair_kernel(
     const float* __restrict__ smoothing) {
   __shared__ FinishShared shared[kWaves];
   __shared__ __align__(16) uint32_t qwords[kWaves][4][kDim / 4];  // [c][k/4]
+  __shared__ __align__(16) int32_t projected[kWaves][kDim][4];    // [value][c]
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const uint32_t state = blockIdx.x * kWaves + wave;
@@ -598,12 +621,13 @@ __global__ __launch_bounds__(kThreads) void fused_decode_pair_kernel(
   if (p >= kWindow) return;
 
   // The small operands first, then the codes (the bulk of the traffic):
-  // memory returns in issue order, so the prepare waits only for the small
-  // operands while the codes are in flight.  Lane owns keys 16*kq..+15 of
-  // value rows r8 + 8j.
+  // memory returns in issue order, so the prepare and the key staging wait
+  // only for the small operands while the codes are in flight.  Lane owns
+  // keys 16*kq..+15 of value rows r8 + 8j.
   const VectorWords words = load_vector_words(in, state, lane);
   const float2 sm = load_smoothing(smoothing, state, lane);
   const float gate_lane = load_gate_lane(fa, state, p, lane);
+  const KeyWords keys = load_key_words(fa, state, p, lane);
   const int kq = lane & 7;
   const int r8 = lane >> 3;
   const int8_t* codes = residual + static_cast<uint64_t>(state) * kTile;
@@ -621,6 +645,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_pair_kernel(
   int high[2][2], low[2][2];
   float ds[4];
   split_pair(pair, high, low, ds);
+  stage_keys(shared[wave], keys, p, lane);
   // Column c of the quantized vectors: 0 = hi0, 1 = lo0, 2 = hi1, 3 = lo1.
   // Lane owns rows 2*lane, 2*lane+1: two bytes of word (2*lane)/4.
   {
@@ -664,17 +689,17 @@ __global__ __launch_bounds__(kThreads) void fused_decode_pair_kernel(
   // Lane holds values r8 + 8 * (2 * kq + e); the finish wants 2 * lane + e.
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    *reinterpret_cast<int4*>(&shared[wave].projected[r8 + 8 * (2 * kq + e)][0]) =
+    *reinterpret_cast<int4*>(&projected[wave][r8 + 8 * (2 * kq + e)][0]) =
         make_int4(acc[0][e], acc[1][e], acc[2][e], acc[3][e]);
   }
   wave_lds_sync();
   int32_t P[2][4];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const int4 w = *reinterpret_cast<const int4*>(&shared[wave].projected[2 * lane + e][0]);
+    const int4 w = *reinterpret_cast<const int4*>(&projected[wave][2 * lane + e][0]);
     P[e][0] = w.x; P[e][1] = w.y; P[e][2] = w.z; P[e][3] = w.w;
   }
-  finish_state(fa, shared[wave], v, state, p, lane, P, ds, gate_lane);
+  finish_state<true>(fa, shared[wave], v, state, p, lane, P, ds, gate_lane);
 }
 
 }  // namespace
