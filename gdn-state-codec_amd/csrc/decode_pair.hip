@@ -23,6 +23,7 @@
 #include "codec_math.h"
 #include "decode_pair.h"
 #include "gdn_state_codec_window.h"
+#include "lane_exchange.h"
 #include "launch.h"
 #include "stream_memory.h"
 #include "window_common.h"
@@ -33,37 +34,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kPairColumns = 16;  // quantized / projected row width
-
-// Cross-lane steps by DPP on the VALU rather than ds_bpermute through the
-// LDS unit.  dpp<ctrl, row_mask>(x): a lane whose source is outside its row,
-// or whose row is masked off, keeps its own x.
-template <int kCtrl, int kRowMask = 0xF>
-__device__ __forceinline__ int dpp(int x) {
-  return __builtin_amdgcn_update_dpp(x, x, kCtrl, kRowMask, 0xF, false);
-}
-constexpr int kQuadSwap1 = 0xB1;    // quad_perm [1,0,3,2]: lane ^ 1
-constexpr int kQuadSwap2 = 0x4E;    // quad_perm [2,3,0,1]: lane ^ 2
-constexpr int kQuadReverse = 0x1B;  // quad_perm [3,2,1,0]: lane ^ 3
-constexpr int kHalfMirror = 0x141;  // row_half_mirror: lane 7 - lane within 8
-
-// Value of lane ^ 4: (lane ^ 3) then 7 - that, within each group of 8.
-__device__ __forceinline__ int from_lane_xor4(int x) {
-  return dpp<kHalfMirror>(dpp<kQuadReverse>(x));
-}
-
-// Maximum over the wavefront, in every lane (fmaxf, so the order of the
-// comparisons cannot change the result): row prefixes by row_shr 1, 2, 4, 8,
-// rows merged by row_bcast 15 and 31, then lane 63 read back.
-__device__ __forceinline__ float wave_max_dpp(float x) {
-  const auto step = [](float v, int other) { return fmaxf(v, __int_as_float(other)); };
-  x = step(x, dpp<0x111>(__float_as_int(x)));
-  x = step(x, dpp<0x112>(__float_as_int(x)));
-  x = step(x, dpp<0x114>(__float_as_int(x)));
-  x = step(x, dpp<0x118>(__float_as_int(x)));
-  x = step(x, dpp<0x142, 0xA>(__float_as_int(x)));
-  x = step(x, dpp<0x143, 0xC>(__float_as_int(x)));
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
-}
 
 // Vector quantizer rounding of the reference: add +-0.5, clamp, truncate.
 __device__ __forceinline__ int pair_round(float value) {
@@ -81,7 +51,7 @@ __device__ __forceinline__ void split_pair(const float (&pair)[2][2],
                                            float (&scale)[4]) {
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
-    const float m = wave_max_dpp(fmaxf(fabsf(pair[c][0]), fabsf(pair[c][1])));
+    const float m = wave_max_valu(fmaxf(fabsf(pair[c][0]), fabsf(pair[c][1])));
     scale[c] = m > 1.0e-20f ? m / 127.0f : 1.0f;
   }
   float residual_max[2];
@@ -94,7 +64,7 @@ __device__ __forceinline__ void split_pair(const float (&pair)[2][2],
       const float residual = pair[c][e] - static_cast<float>(high[c][e]) * scale[c];
       m = fmaxf(m, fabsf(residual));
     }
-    residual_max[c] = wave_max_dpp(m);
+    residual_max[c] = wave_max_valu(m);
   }
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
@@ -483,7 +453,7 @@ __global__ __launch_bounds__(kThreads) void prepare_vector_kernel(
     x[e] = half_bits_to_float(input[row * kPairColumns]) * axis_scale[row];
     m = fmaxf(m, fabsf(x[e]));
   }
-  m = wave_max_dpp(m);
+  m = wave_max_valu(m);
   const float scale = m > 1.0e-20f ? m / 127.0f : 1.0f;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
@@ -584,26 +554,11 @@ __global__ __launch_bounds__(kThreads) void finish_pair_kernel(
 // Integer analogue of the decode projection's pairwise lane reduction.
 __device__ __forceinline__ void reduce16_over_8_lanes_int(int32_t (&p)[16], int lane) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const bool up = (lane & 4) != 0;
-    const int32_t send = up ? p[i] : p[i + 8];
-    const int32_t keep = up ? p[i + 8] : p[i];
-    p[i] = keep + from_lane_xor4(send);
-  }
+  for (int i = 0; i < 8; ++i) p[i] = fold<4>(p[i], p[i + 8], lane);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const bool up = (lane & 2) != 0;
-    const int32_t send = up ? p[i] : p[i + 4];
-    const int32_t keep = up ? p[i + 4] : p[i];
-    p[i] = keep + dpp<kQuadSwap2>(send);
-  }
+  for (int i = 0; i < 4; ++i) p[i] = fold<2>(p[i], p[i + 4], lane);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const bool up = (lane & 1) != 0;
-    const int32_t send = up ? p[i] : p[i + 2];
-    const int32_t keep = up ? p[i + 2] : p[i];
-    p[i] = keep + dpp<kQuadSwap1>(send);
-  }
+  for (int i = 0; i < 2; ++i) p[i] = fold<1>(p[i], p[i + 2], lane);
 }
 
 // prepare + projection + finish for one state per wavefront.

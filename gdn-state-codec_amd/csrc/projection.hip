@@ -26,6 +26,7 @@
 
 #include "codec_math.h"
 #include "bf16_operands.h"
+#include "lane_exchange.h"
 #include "launch.h"
 #include "stream_memory.h"
 
@@ -45,11 +46,23 @@ __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
 
 // ------------------------------------------------------------------ decode
 
-// Adds partner halves so that, over the 3 lane bits selected by masks
-// m2 > m1 > m0, 16 partials reduce to 2 per lane: the lane keeps entries
-// 2 * idx + {0, 1} where idx = 4*bit(m2) + 2*bit(m1) + bit(m0).
-__device__ __forceinline__ void reduce16_over_8_lanes(float (&p)[16], int lane,
-                                                      int m2, int m1, int m0) {
+// Adds partner halves so that, over the 3 lane bits M2 > M1 > M0, 16 partials
+// reduce to 2 per lane: the lane keeps entries 2 * idx + {0, 1} where
+// idx = 4*bit(M2) + 2*bit(M1) + bit(M0).
+template <int M2, int M1, int M0>
+__device__ __forceinline__ void reduce16_over_8_lanes(float (&p)[16], int lane) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p[i] = fold<M2>(p[i], p[i + 8], lane);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = fold<M1>(p[i], p[i + 4], lane);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) p[i] = fold<M0>(p[i], p[i + 2], lane);
+}
+
+// The same reduction through ds_bpermute, for the [key][value] decode kernel:
+// at its 64-VGPR limit the VALU exchanges spill.
+__device__ __forceinline__ void reduce16_over_8_lanes_shuffle(float (&p)[16], int lane,
+                                                              int m2, int m1, int m0) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const bool up = (lane & m2) != 0;
@@ -123,7 +136,7 @@ __global__ __launch_bounds__(kThreads, 8) void decode_projection_kernel(
       acc[j] = a;
     }
     // Sum the 8 key chunks (lane bits 0..2); the lane keeps rows j = 2kq + e.
-    reduce16_over_8_lanes(acc, lane, 4, 2, 1);
+    reduce16_over_8_lanes<4, 2, 1>(acc, lane);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int v = r8 + 8 * (2 * kq + e);
@@ -155,7 +168,7 @@ __global__ __launch_bounds__(kThreads, 8) void decode_projection_kernel(
       }
     }
     // Sum the 8 key groups (lane bits 3..5); the lane keeps values 2kr + e.
-    reduce16_over_8_lanes(acc, lane, 32, 16, 8);
+    reduce16_over_8_lanes_shuffle(acc, lane, 32, 16, 8);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int v = 16 * vc + 2 * kr + e;

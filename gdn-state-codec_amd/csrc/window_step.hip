@@ -29,6 +29,7 @@
 
 #include "codec_math.h"
 #include "gdn_state_codec_window.h"
+#include "lane_exchange.h"
 #include "launch.h"
 #include "stream_memory.h"
 #include "window_common.h"
@@ -71,30 +72,15 @@ __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
 }
 
 // Pairwise combination over 3 lane bits: 16 partials per lane become 2 per
-// lane holding entries 2 * idx + {0, 1}, idx = 4*bit(m2) + 2*bit(m1) + bit(m0).
-__device__ __forceinline__ void reduce16_over_8_lanes(float (&p)[16], int lane,
-                                                      int m2, int m1, int m0) {
+// lane holding entries 2 * idx + {0, 1}, idx = 4*bit(M2) + 2*bit(M1) + bit(M0).
+template <int M2, int M1, int M0>
+__device__ __forceinline__ void reduce16_over_8_lanes(float (&p)[16], int lane) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const bool up = (lane & m2) != 0;
-    const float send = up ? p[i] : p[i + 8];
-    const float keep = up ? p[i + 8] : p[i];
-    p[i] = keep + __shfl_xor(send, m2);
-  }
+  for (int i = 0; i < 8; ++i) p[i] = fold<M2>(p[i], p[i + 8], lane);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const bool up = (lane & m1) != 0;
-    const float send = up ? p[i] : p[i + 4];
-    const float keep = up ? p[i + 4] : p[i];
-    p[i] = keep + __shfl_xor(send, m1);
-  }
+  for (int i = 0; i < 4; ++i) p[i] = fold<M1>(p[i], p[i + 4], lane);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const bool up = (lane & m0) != 0;
-    const float send = up ? p[i] : p[i + 2];
-    const float keep = up ? p[i + 2] : p[i];
-    p[i] = keep + __shfl_xor(send, m0);
-  }
+  for (int i = 0; i < 2; ++i) p[i] = fold<M0>(p[i], p[i + 2], lane);
 }
 
 // Reduce-scatter of N partial sums over the 64 lanes: log2(N) halving steps
@@ -104,24 +90,22 @@ template <int N, int kMask>
 __device__ __forceinline__ void halve(float* v, int lane) {
   if constexpr (N > 1) {
     constexpr int n = N / 2;
-    const bool up = (lane & kMask) != 0;
 #pragma unroll
-    for (int i = 0; i < n; ++i) {
-      const float send = up ? v[i] : v[i + n];
-      const float keep = up ? v[i + n] : v[i];
-      v[i] = keep + __shfl_xor(send, kMask);
-    }
+    for (int i = 0; i < n; ++i) v[i] = fold<kMask>(v[i], v[i + n], lane);
     halve<n, kMask / 2>(v, lane);
   }
+}
+
+template <int kMask>
+__device__ __forceinline__ float sum_low_bits(float x) {
+  if constexpr (kMask >= 1) return sum_low_bits<kMask / 2>(add_partner<kMask>(x));
+  return x;
 }
 
 template <int N>
 __device__ __forceinline__ float reduce_scatter(float (&v)[N], int lane) {
   halve<N, 32>(v, lane);
-  float x = v[0];
-#pragma unroll
-  for (int mask = 32 / N; mask >= 1; mask >>= 1) x += __shfl_xor(x, mask);
-  return x;
+  return sum_low_bits<32 / N>(v[0]);
 }
 
 template <int kVariant>
@@ -217,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
   out1 = query1 * g;
   *reinterpret_cast<float2*>(&weights[wave][0][k0]) = make_float2(sm.x * read0, sm.y * read1);
   *reinterpret_cast<float2*>(&weights[wave][1][k0]) = make_float2(sm.x * out0, sm.y * out1);
-  const float update = wave_sum(write0 * query0 + write1 * query1);
+  const float update = wave_sum_valu(write0 * query0 + write1 * query1);
 
   // Gate products: suffix_j = prod_{i > j} gate_i over the p stored records,
   // in descending i; the 1.0 of lanes j >= p leaves every product unchanged.
@@ -303,8 +287,8 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
       acc_read[j] = ar;
       acc_out[j] = ao;
     }
-    reduce16_over_8_lanes(acc_read, lane, 4, 2, 1);
-    reduce16_over_8_lanes(acc_out, lane, 4, 2, 1);
+    reduce16_over_8_lanes<4, 2, 1>(acc_read, lane);
+    reduce16_over_8_lanes<4, 2, 1>(acc_out, lane);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int v = row8 + 8 * (2 * chunk + e);
@@ -329,8 +313,8 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
         acc_out[i] = fmaf(c, wo, acc_out[i]);
       }
     }
-    reduce16_over_8_lanes(acc_read, lane, 32, 16, 8);
-    reduce16_over_8_lanes(acc_out, lane, 32, 16, 8);
+    reduce16_over_8_lanes<32, 16, 8>(acc_read, lane);
+    reduce16_over_8_lanes<32, 16, 8>(acc_out, lane);
     // values 16*chunk + 2*row8 + {0, 1}: adjacent, one 8-byte LDS store each.
     const int v = 16 * chunk + 2 * row8;
     *reinterpret_cast<float2*>(&readouts[wave][0][v]) = make_float2(acc_read[0], acc_read[1]);
