@@ -106,16 +106,17 @@ def _probe_library():
     path = _native.library_dir() / "libgdn_state_codec_hbm_probe.so"
     lib = ctypes.CDLL(str(path))
     for name in ("gdn_hbm_probe_copy", "gdn_hbm_probe_read"):
-        getattr(lib, name).argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint64]
+        getattr(lib, name).argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint64, ctypes.c_uint32]
         getattr(lib, name).restype = ctypes.c_int32
-    lib.gdn_hbm_probe_write.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint64]
+    lib.gdn_hbm_probe_write.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint64, ctypes.c_uint32]
     lib.gdn_hbm_probe_write.restype = ctypes.c_int32
     lib.gdn_hbm_probe_grid.restype = ctypes.c_uint32
     return lib
 
 
 def bench_hbm_probe(repeats: int = 5):
-    """Sustained HBM bandwidth of plain streaming kernels (4 GiB buffers)."""
+    """Sustained HBM bandwidth of plain streaming kernels (4 GiB buffers), with
+    plain accesses and with the nontemporal hint the codec kernels use."""
     import torch
 
     lib = _probe_library()
@@ -125,26 +126,27 @@ def bench_hbm_probe(repeats: int = 5):
     dst = torch.empty_like(src)
     sink = torch.empty(lib.gdn_hbm_probe_grid() * 256, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
-    launches = {
-        "copy": (lambda: lib.gdn_hbm_probe_copy(stream, src.data_ptr(), dst.data_ptr(), nbytes),
-                 2 * nbytes),
-        "read": (lambda: lib.gdn_hbm_probe_read(stream, src.data_ptr(), sink.data_ptr(), nbytes),
-                 nbytes),
-        "write": (lambda: lib.gdn_hbm_probe_write(stream, dst.data_ptr(), nbytes), nbytes),
-    }
     out = {}
-    for name, (fn, moved) in launches.items():
-        for _ in range(2):
-            assert fn() == 0
-        pairs = []
-        for _ in range(repeats):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            assert fn() == 0
-            b.record()
-            pairs.append((a, b))
-        ms = sorted(_events_ms(pairs))[len(pairs) // 2]
-        out[f"{name}_GBps"] = moved / (ms * 1e-3) / 1e9
+    for mode, suffix in ((0, ""), (1, "_nt")):
+        launches = {
+            "copy": (lambda: lib.gdn_hbm_probe_copy(stream, src.data_ptr(), dst.data_ptr(), nbytes,
+                                                    mode), 2 * nbytes),
+            "read": (lambda: lib.gdn_hbm_probe_read(stream, src.data_ptr(), sink.data_ptr(), nbytes,
+                                                    mode), nbytes),
+            "write": (lambda: lib.gdn_hbm_probe_write(stream, dst.data_ptr(), nbytes, mode), nbytes),
+        }
+        for name, (fn, moved) in launches.items():
+            for _ in range(2):
+                assert fn() == 0
+            pairs = []
+            for _ in range(repeats):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                assert fn() == 0
+                b.record()
+                pairs.append((a, b))
+            ms = sorted(_events_ms(pairs))[len(pairs) // 2]
+            out[f"{name}{suffix}_GBps"] = moved / (ms * 1e-3) / 1e9
     del src, dst, sink
     _log("hbm probe: " + ", ".join(f"{k}={v:.0f}" for k, v in out.items()))
     return out

@@ -2,17 +2,38 @@
 //
 // Three streaming kernels with the codec's access granularity (16-byte
 // vector loads/stores, 256-thread workgroups, one contiguous 4 KiB chunk per
-// workgroup iteration): copy, read-only and write-only.  They give the
-// bandwidth this GPU actually sustains, and the copy kernel is the known-size
-// reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings.
+// workgroup iteration): copy, read-only and write-only, each with plain and
+// with nontemporal accesses (the hint the codec kernels use).  They give the
+// bandwidth this GPU actually sustains, and the plain copy kernel is the
+// known-size reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "stream_memory.h"
+
 namespace {
+
+template <bool kNontemporal>
+__device__ __forceinline__ uint4 load16(const uint4* p) {
+  if constexpr (kNontemporal) return gdn::stream_load(p);
+  return *p;
+}
+
+template <bool kNontemporal>
+__device__ __forceinline__ void store16(uint4* p, uint4 v) {
+  if constexpr (kNontemporal) {
+    gdn::stream_store(reinterpret_cast<float4*>(p),
+                      make_float4(__uint_as_float(v.x), __uint_as_float(v.y),
+                                  __uint_as_float(v.z), __uint_as_float(v.w)));
+  } else {
+    *p = v;
+  }
+}
 
 constexpr int kThreads = 256;
 constexpr int kUnroll = 4;  // 16-byte accesses in flight per thread
 
+template <bool kNontemporal>
 __global__ __launch_bounds__(kThreads) void copy_kernel(const uint4* __restrict__ src,
                                                         uint4* __restrict__ dst,
                                                         uint64_t vectors) {
@@ -24,16 +45,17 @@ __global__ __launch_bounds__(kThreads) void copy_kernel(const uint4* __restrict_
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
-      if (i < vectors) v[u] = src[i];
+      if (i < vectors) v[u] = load16<kNontemporal>(src + i);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
-      if (i < vectors) dst[i] = v[u];
+      if (i < vectors) store16<kNontemporal>(dst + i, v[u]);
     }
   }
 }
 
+template <bool kNontemporal>
 __global__ __launch_bounds__(kThreads) void read_kernel(const uint4* __restrict__ src,
                                                         uint32_t* __restrict__ sink,
                                                         uint64_t vectors) {
@@ -46,7 +68,7 @@ __global__ __launch_bounds__(kThreads) void read_kernel(const uint4* __restrict_
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
       if (i < vectors) {
-        const uint4 v = src[i];
+        const uint4 v = load16<kNontemporal>(src + i);
         acc ^= v.x ^ v.y ^ v.z ^ v.w;
       }
     }
@@ -55,6 +77,7 @@ __global__ __launch_bounds__(kThreads) void read_kernel(const uint4* __restrict_
   sink[static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x] = acc;
 }
 
+template <bool kNontemporal>
 __global__ __launch_bounds__(kThreads) void write_kernel(uint4* __restrict__ dst,
                                                          uint64_t vectors,
                                                          uint32_t value) {
@@ -66,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void write_kernel(uint4* __restrict__ dst
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
-      if (i < vectors) dst[i] = v;
+      if (i < vectors) store16<kNontemporal>(dst + i, v);
     }
   }
 }
@@ -77,10 +100,12 @@ __global__ __launch_bounds__(kThreads) void write_kernel(uint4* __restrict__ dst
 // times over; the sink for the read probe must hold kProbeGrid * 256 words.
 extern "C" uint32_t gdn_hbm_probe_grid() { return 256u * 64u; }
 
+// mode 0: plain accesses; mode 1: nontemporal.
 extern "C" int32_t gdn_hbm_probe_copy(void* stream, const void* src, void* dst,
-                                      uint64_t bytes) {
-  if (src == nullptr || dst == nullptr || bytes % 16 != 0) return 1;
-  hipLaunchKernelGGL(copy_kernel, dim3(gdn_hbm_probe_grid()), dim3(kThreads), 0,
+                                      uint64_t bytes, uint32_t mode) {
+  if (src == nullptr || dst == nullptr || bytes % 16 != 0 || mode > 1) return 1;
+  const auto kernel = mode ? copy_kernel<true> : copy_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3(gdn_hbm_probe_grid()), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream),
                      static_cast<const uint4*>(src), static_cast<uint4*>(dst),
                      bytes / 16);
@@ -88,18 +113,21 @@ extern "C" int32_t gdn_hbm_probe_copy(void* stream, const void* src, void* dst,
 }
 
 extern "C" int32_t gdn_hbm_probe_read(void* stream, const void* src, void* sink,
-                                      uint64_t bytes) {
-  if (src == nullptr || sink == nullptr || bytes % 16 != 0) return 1;
-  hipLaunchKernelGGL(read_kernel, dim3(gdn_hbm_probe_grid()), dim3(kThreads), 0,
+                                      uint64_t bytes, uint32_t mode) {
+  if (src == nullptr || sink == nullptr || bytes % 16 != 0 || mode > 1) return 1;
+  const auto kernel = mode ? read_kernel<true> : read_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3(gdn_hbm_probe_grid()), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream),
                      static_cast<const uint4*>(src), static_cast<uint32_t*>(sink),
                      bytes / 16);
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 
-extern "C" int32_t gdn_hbm_probe_write(void* stream, void* dst, uint64_t bytes) {
-  if (dst == nullptr || bytes % 16 != 0) return 1;
-  hipLaunchKernelGGL(write_kernel, dim3(gdn_hbm_probe_grid()), dim3(kThreads), 0,
+extern "C" int32_t gdn_hbm_probe_write(void* stream, void* dst, uint64_t bytes,
+                                       uint32_t mode) {
+  if (dst == nullptr || bytes % 16 != 0 || mode > 1) return 1;
+  const auto kernel = mode ? write_kernel<true> : write_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3(gdn_hbm_probe_grid()), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<uint4*>(dst),
                      bytes / 16, 0x3F800000u);
   return hipGetLastError() == hipSuccess ? 0 : 5;

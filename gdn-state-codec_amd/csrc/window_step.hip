@@ -108,6 +108,8 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[N], int lane) {
   return sum_low_bits<32 / N>(v[0]);
 }
 
+constexpr int kEarlyRows = 12;  // code rows issued before phase 1 (of 16)
+
 template <int kVariant>
 __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
   constexpr bool kValueKey = kVariant != kStepF16;
@@ -117,6 +119,9 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
   // [0, 16): record read-side coefficients, [16, 32): output side,
   // [32, 36) / [36, 40): compensator read / output projections.
   __shared__ float coefficients[kWaves][2 * kWindow + 2 * kRank];
+  // Record corrections j < p of this lane's two values, parked from phase 1
+  // to phase 3 so that they hold no registers during phase 2.
+  __shared__ uint32_t parked_corrections[kWaves][kWindow - 1][64];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -161,21 +166,37 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
   // Lane j < p holds gate j (one load, issued before the codes so that phase 1
   // does not wait for them); the other lanes hold 1.0.
   const float gate_lane = lane < static_cast<int>(p) ? a.record_decay[record_base + lane] : 1.0f;
+  // Phase-3 record corrections for values k0, k0+1: loaded before the codes
+  // too, and parked in LDS by phase 1.
+  uint32_t correction_word[kWindow - 1];
+#pragma unroll
+  for (int j = 0; j < kWindow - 1; ++j) {
+    correction_word[j] = j < static_cast<int>(p)
+        ? *reinterpret_cast<const uint32_t*>(a.record_corrections + (record_base + j) * kDim + k0)
+        : 0u;
+  }
   // Lane (c, r) = (lane & 7, lane >> 3) reads bytes 16c..16c+15 of rows r + 8j.
   const int8_t* codes = a.residual + static_cast<uint64_t>(state) * kTile;
   const int chunk = lane & 7;
   const int row8 = lane >> 3;
+  // Rows 0..11 now, rows 12..15 after phase 1: with all 16 in flight through
+  // phase 1 the kernel needs more than 128 VGPRs and runs 3 wavefronts per
+  // SIMD instead of 4.
   uint4 row[16];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < kEarlyRows; ++j) {
     row[j] = stream_load(reinterpret_cast<const uint4*>(codes + (row8 + 8 * j) * kDim + 16 * chunk));
   }
-  // Every load is issued before any phase-1 arithmetic: without this barrier
+  // The loads above are issued before any phase-1 arithmetic: without this barrier
   // the scheduler hoists phase-1 math, with its waits for the small operands,
   // above the code loads, and the 16 KiB stream starts a round trip late.
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- phase 1: vectors, update, compensator and record projections --------
+#pragma unroll
+  for (int j = 0; j < kWindow - 1; ++j) {
+    if (j < static_cast<int>(p)) parked_corrections[wave][j][lane] = correction_word[j];
+  }
   float read0, read1, out0, out1, write0, write1, query0, query1;
   uint32_t record_key_bits;
   if constexpr (kVariant == kStepF16) {
@@ -203,13 +224,16 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
   *reinterpret_cast<float2*>(&weights[wave][1][k0]) = make_float2(sm.x * out0, sm.y * out1);
   const float update = wave_sum_valu(write0 * query0 + write1 * query1);
 
-  // Gate products: suffix_j = prod_{i > j} gate_i over the p stored records,
-  // in descending i; the 1.0 of lanes j >= p leaves every product unchanged.
+  // Gate products in descending record order, the 1.0 of lanes j >= p leaving
+  // every product unchanged: boundary_suffix = prod_i gate_i, and
+  // lane_suffix = prod_{i > j} gate_i for the record j = (lane >> 1) & 15
+  // whose coefficient this lane scales.
+  const int lane_record = (lane >> 1) & (kWindow - 1);
   float boundary_suffix = 1.0f;
-  float suffix[kWindow];
+  float lane_suffix = 1.0f;
 #pragma unroll
   for (int j = kWindow - 1; j >= 0; --j) {
-    suffix[j] = boundary_suffix;
+    if (j == lane_record) lane_suffix = boundary_suffix;
     boundary_suffix *= __builtin_bit_cast(
         float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gate_lane), j));
   }
@@ -226,12 +250,7 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
       partial[kWindow + j] = b0 * out0 + b1 * out1;
     }
     const float total = reduce_scatter(partial, lane);
-    const int index = lane >> 1;
-    const int j = index & (kWindow - 1);
-    float sfx = 1.0f;
-#pragma unroll
-    for (int jj = 0; jj < kWindow; ++jj) sfx = jj == j ? suffix[jj] : sfx;
-    if ((lane & 1) == 0) coefficients[wave][index] = total * sfx;
+    if ((lane & 1) == 0) coefficients[wave][lane >> 1] = total * lane_suffix;
   }
   if constexpr (kCompensated) {
     const uint32_t words[4] = {comp_key.x, comp_key.y, comp_key.z, comp_key.w};
@@ -247,14 +266,11 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
     if ((lane & 7) == 0) coefficients[wave][2 * kWindow + (lane >> 3)] = total * boundary_suffix;
   }
 
-  // Phase-3 operands for values k0, k0+1, in flight during phase 2.
-  uint32_t correction_word[kWindow];
 #pragma unroll
-  for (int j = 0; j < kWindow; ++j) {
-    correction_word[j] = j < static_cast<int>(p)
-        ? *reinterpret_cast<const uint32_t*>(a.record_corrections + (record_base + j) * kDim + k0)
-        : 0u;
+  for (int j = kEarlyRows; j < 16; ++j) {
+    row[j] = stream_load(reinterpret_cast<const uint4*>(codes + (row8 + 8 * j) * kDim + 16 * chunk));
   }
+  // Phase-3 operands for values k0, k0+1, in flight during phase 2.
   const float2 scale = *reinterpret_cast<const float2*>(a.scales + vector_base + k0);
   const uint32_t value_word = *reinterpret_cast<const uint32_t*>(a.values + vector_base + k0);
   uint4 comp_value = make_uint4(0u, 0u, 0u, 0u);
@@ -346,9 +362,10 @@ __global__ __launch_bounds__(kThreads) void window_step_kernel(StepArgs a) {
       }
     }
 #pragma unroll
-    for (int j = 0; j < kWindow; ++j) {
+    for (int j = 0; j < kWindow - 1; ++j) {
       if (j < static_cast<int>(p)) {
-        const float c = half_bits_to_float((correction_word[j] >> (16 * e)) & 0xFFFFu);
+        const uint32_t word = parked_corrections[wave][j][lane];
+        const float c = half_bits_to_float((word >> (16 * e)) & 0xFFFFu);
         state_read = fmaf(c, coefficients[wave][j], state_read);
         output_read = fmaf(c, coefficients[wave][kWindow + j], output_read);
       }
