@@ -128,3 +128,62 @@ def test_power_refit_is_bit_exact(device, iterations):
     assert_same(from_device(do, out), ref_out, OUT_NAMES)
     assert_same(from_device(d, buf), ref, buf.keys())
     assert dw.cpu().numpy().tobytes() == ref_ws.tobytes()
+
+
+def _full_batch(seed):
+    """B = 256 sequences x 32 value heads, the bench's refit batch: every
+    seventeenth state is not full (positions 0..15 in turn) and must come back
+    untouched."""
+    states = 8192
+    positions = [16] * states
+    for n, s in enumerate(range(0, states, 17)):
+        positions[s] = n % 16
+    return states, WG.window_buffers(states, seed, VK, positions=positions)
+
+
+def _subset(buffers: dict, idx):
+    return {k: np.ascontiguousarray(v[idx]) for k, v in buffers.items()}
+
+
+def test_quant_only_refit_full_batch_is_bit_exact(device):
+    """All 8192 states of one launch against the oracle, every output bit."""
+    states, buf = _full_batch(73)
+    print(f"quant-only refit states={states}", flush=True)
+    out = sentinel_outputs(states)
+    d, do = to_device(buf, device), to_device(out, device)
+    workspace = torch.zeros(16, dtype=torch.float32, device=device)
+    assert native().window_boundary_launch_v1(
+        stream(), *window_ptrs(d), *out_ptrs(do), workspace.data_ptr(), states, 0) == 0
+    torch.cuda.synchronize()
+    ref, ref_out = WG.copy_buffers(buf), WG.copy_buffers(out)
+    W.window_boundary_quant_only(ref, ref_out)
+    assert_same(from_device(do, out), ref_out, OUT_NAMES)
+    assert_same(from_device(d, buf), ref, buf.keys())
+
+
+def test_power_refit_full_batch(device):
+    """One 4-iteration launch over 8192 states: every fourth state against the
+    oracle (outputs, records, positions and its workspace rows), and every
+    state that is not full left untouched, its outputs and workspace too."""
+    states, buf = _full_batch(79)
+    print(f"power refit states={states}", flush=True)
+    out = sentinel_outputs(states)
+    d, do = to_device(buf, device), to_device(out, device)
+    dw = torch.full((states, 128, 128), 7.0, dtype=torch.float32, device=device)
+    assert native().window_boundary_launch_v1(
+        stream(), *window_ptrs(d), *out_ptrs(do), dw.data_ptr(), states, 4) == 0
+    torch.cuda.synchronize()
+    got_out, got_buf = from_device(do, out), from_device(d, buf)
+    got_ws = dw.cpu().numpy()
+    idx = np.arange(0, states, 4)
+    ref, ref_out = _subset(buf, idx), _subset(out, idx)
+    ref_ws = np.full((idx.size, 128, 128), 7.0, np.float32)
+    W.window_boundary_power(ref, ref_out, ref_ws, 4)
+    assert_same(_subset(got_out, idx), ref_out, OUT_NAMES)
+    assert_same(_subset(got_buf, idx), ref, buf.keys())
+    assert got_ws[idx].tobytes() == ref_ws.tobytes()
+    waiting = np.flatnonzero(buf["positions"][:, 0] < 16)
+    assert waiting.size == len(range(0, states, 17))
+    assert_same(_subset(got_out, waiting), _subset(out, waiting), OUT_NAMES)
+    assert_same(_subset(got_buf, waiting), _subset(buf, waiting), buf.keys())
+    assert (got_ws[waiting] == 7.0).all()

@@ -70,3 +70,85 @@ def test_out_of_range_slot_ids_are_skipped(device):
     assert not got[:, 1:4].any()  # untouched zero-initialised outputs
     oc, _, _ = oracle.pool_encode(pool, np.array([0, -1, -1, -1, 3], np.int32), KV)
     assert got.tobytes() == oc.tobytes()
+
+
+def test_full_config5_bf16_pool(device):
+    """BASELINE config 5 at full size, in the provider's [value][key] layout:
+    a [30][2048][32] bf16 pool (64.4 GB) of Student-t(3) * 0.05 entries with
+    2% all-zero heads, 512 unique random slot ids of which 26 are -1.  After
+    pool_encode and a pool_decode back into the same pool: codes within +-127
+    and every live column reaching 127; zero heads with zero codes,
+    s = sqrtf(1e-8) and scale 0; padding entries of the encoded batch
+    untouched; slots outside the batch unchanged; and 96 sampled tiles
+    bit-exact against the oracle in both directions."""
+    print("full config-5 bf16 pool", flush=True)
+    layers, slots, heads, batch = 30, 2048, 32, 512
+    gen = torch.Generator(device=device)
+    gen.manual_seed(55)
+    pool = torch.empty((layers, slots, heads, 128, 128), dtype=torch.bfloat16, device=device)
+    for layer in range(layers):
+        for part in range(0, slots, 256):
+            shape = (256, heads, 128, 128)
+            z = torch.randn(shape, generator=gen, device=device)
+            chi = torch.zeros(shape, device=device)
+            for _ in range(3):
+                w = torch.randn(shape, generator=gen, device=device)
+                chi.addcmul_(w, w)
+            pool[layer, part:part + 256] = (z * torch.rsqrt(chi / 3) * 0.05).to(torch.bfloat16)
+            del z, chi, w
+    zero = torch.rand((layers, slots, heads), generator=gen, device=device) < 0.02
+    pool[zero] = 0
+    ids = torch.randperm(slots, generator=gen, device=device)[:batch].to(torch.int32)
+    ids[torch.randperm(batch, generator=gen, device=device)[:26]] = -1
+    live = ids >= 0
+    outside = torch.ones(slots, dtype=torch.bool, device=device)
+    outside[ids[live].long()] = False
+    outside_slots = torch.nonzero(outside).flatten()[:64]
+    before = pool[:, outside_slots].view(torch.int16).to(torch.int64).sum(dim=(2, 3, 4))
+
+    codes = torch.full((layers, batch, heads, 128, 128), 0x55, dtype=torch.int8, device=device)
+    s = torch.full((layers, batch, heads, 128), -1.0, dtype=torch.float32, device=device)
+    sc = torch.full((layers, batch, heads, 128), -1.0, dtype=torch.float32, device=device)
+    codec.pool_encode(pool, ids, VK, codes, s, sc)
+    torch.cuda.synchronize()
+
+    # Sampled tiles, taken before the decode overwrites the pool.
+    g = datagen.rng(56)
+    live_entries = torch.nonzero(live).flatten().cpu().numpy()
+    picks = [(int(g.integers(layers)), int(g.choice(live_entries)), int(g.integers(heads)))
+             for _ in range(96)]
+    slot_of = ids.cpu().numpy()
+    src = np.stack([pool[l, slot_of[b], h].view(torch.int16).cpu().numpy().view(np.uint16)
+                    for l, b, h in picks])
+    ocodes, os_, osc = oracle.encode_heads(oracle.bf16_to_f32(src).reshape(-1, 128, 128), VK,
+                                           threads=8)
+    for n, (l, b, h) in enumerate(picks):
+        assert codes[l, b, h].cpu().numpy().tobytes() == ocodes[n].tobytes(), (l, b, h)
+        assert s[l, b, h].cpu().numpy().tobytes() == os_[n].tobytes(), (l, b, h)
+        assert sc[l, b, h].cpu().numpy().tobytes() == osc[n].tobytes(), (l, b, h)
+
+    pad = torch.nonzero(~live).flatten()
+    assert bool((codes[:, pad] == 0x55).all()) and bool((s[:, pad] == -1).all())
+    assert bool((sc[:, pad] == -1).all())
+    live_idx = torch.nonzero(live).flatten()
+    floor = float(np.sqrt(np.float32(1e-8), dtype=np.float32))
+    for layer in range(layers):
+        c = codes[layer, live_idx]
+        assert int(c.min()) >= -127 and int(c.max()) <= 127
+        col_max = c.abs().amax(dim=3)  # [entries, heads, value]: VK tiles are [value][key]
+        assert bool(((col_max == 127) | (sc[layer, live_idx] == 0)).all()), layer
+        z = zero[layer, ids[live_idx].long()]
+        assert bool((c[z] == 0).all()) and bool((sc[layer, live_idx][z] == 0).all())
+        assert bool((s[layer, live_idx][z] == floor).all())
+        del c, col_max, z
+
+    codec.pool_decode(codes, s, sc, ids, pool, VK)
+    torch.cuda.synchronize()
+    odense = oracle.decode_heads(ocodes, os_, osc, VK, threads=8)
+    expect = oracle.f32_to_bf16(odense.reshape(-1)).reshape(odense.shape)
+    for n, (l, b, h) in enumerate(picks):
+        got = pool[l, slot_of[b], h].view(torch.int16).cpu().numpy().view(np.uint16)
+        assert got.tobytes() == expect[n].tobytes(), (l, b, h)
+    after = pool[:, outside_slots].view(torch.int16).to(torch.int64).sum(dim=(2, 3, 4))
+    assert torch.equal(before, after)
+    del pool, codes, s, sc
