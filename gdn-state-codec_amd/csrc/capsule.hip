@@ -16,8 +16,10 @@
 //
 // SHA-256 is a serial chain per message (FIPS 180-4 section 6.2), so the
 // digest kernel gives each capsule one lane and is bound by integer VALU
-// issue, not HBM: one 64-byte block is ~1.5k VALU instructions.  The pack and
-// unpack kernels move 22-45 KB per state and are HBM-bound.
+// issue, not HBM: a producer wavefront expands each 64-byte block's message
+// schedule and the consumer's round chain is about 900 VALU instructions per
+// block.  The pack and unpack kernels move 22-45 KB per state and are
+// HBM-bound.
 #include <hip/hip_runtime.h>
 #include <float.h>
 #include <stdint.h>

@@ -237,15 +237,21 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
     // min_abs is the smallest NON-ZERO |r|: zeros add nothing to a key sum and
     // divide exactly on both division paths, so they must not force the slow
     // paths (dequantized states hold many exact zeros, one per code 0).
-    float min_abs = INFINITY;
+    // On the bits: (b << 1) drops the sign and keeps the order of the
+    // magnitudes, and subtracting 1 turns a zero into the largest unsigned
+    // value, so one unsigned minimum (v_lshl_add + half a v_min3 per value)
+    // skips the zeros.
+    uint32_t min_key = 0xFFFFFFFFu;
 #pragma unroll
     for (int j = 0; j < kRowsPerThread; ++j) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a = fabsf(x[j][i]);
-        min_abs = fminf(min_abs, a == 0.0f ? INFINITY : a);
+      for (int i = 0; i < 4; i += 2) {
+        const uint32_t a = (__float_as_uint(x[j][i]) << 1) - 1u;
+        const uint32_t b = (__float_as_uint(x[j][i + 1]) << 1) - 1u;
+        min_key = min(min_key, min(a, b));
       }
     }
+    float min_abs = min_key == 0xFFFFFFFFu ? INFINITY : __uint_as_float((min_key + 1u) >> 1);
     if constexpr (kLayout == kKeyValue) {
       double p[kRowsPerThread];
 #pragma unroll
