@@ -25,7 +25,8 @@ CSRC = PACKAGE_DIR / "csrc"
 LIB_DIR = PACKAGE_DIR / "lib"
 OBJ_DIR = LIB_DIR / "obj"
 LIBRARY_NAME = "libstatecentric_gdn_state_codec.so"
-# Bandwidth probes for bench.py only (csrc/bench/); not part of the C-ABI.
+# Probes (csrc/bench/): HBM bandwidth for bench.py and the wavefront-exchange
+# self-check for the tests; not part of the C-ABI.
 PROBE_LIBRARY_NAME = "libgdn_state_codec_hbm_probe.so"
 
 # Reference library names (runtime.py:55-62, 72, 101, 131, 154, 182, 202, 224)
