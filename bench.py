@@ -530,9 +530,10 @@ def cpu_baseline_capsule(target_seconds: float = 8.0):
             out = [C.slot_serialize(buf, s, 1, identity) for s in ids]
         return out
 
+    target = {n: v.copy() for n, v in buf.items()}  # threads restore disjoint states
+
     def restore_some(work):
         ids, reps = work
-        target = {n: v.copy() for n, v in buf.items()}
         bad = 0
         for _ in range(reps):
             for s in ids:
