@@ -175,13 +175,19 @@ __global__ __launch_bounds__(kThreads) void quant_only_refit_kernel(RefitArgs a)
   __syncthreads();
 
   // m[k] = w[k] / s[k] for the wave's 32 columns, kept in registers.
-  float m0[kColumnsPerWave], m1[kColumnsPerWave];
-#pragma unroll
-  for (int c = 0; c < kColumnsPerWave; ++c) {
+  // Markstein's division by the lane's two smoothing values (div_by_reciprocal)
+  // equals IEEE division when s lies in [2^-20, 2^20] and every w is 0 or in
+  // [2^-100, 2^100], so that |w/s| lies in [2^-120, 2^120]; -0 gives +0, which
+  // neither max|m| nor the code rounding can see.  The loop divides that way
+  // and checks the domain as it goes (the smallest non-zero |w| as an unsigned
+  // minimum of (bits << 1) - 1, where a zero becomes the largest value); a
+  // wavefront with a lane outside it computes w again and divides with IEEE
+  // division.
+  const auto boundary_value = [&](int c, float& w0, float& w1) {
     const int v = column0 + c;
     const float factor = factors[v];
-    float w0 = static_cast<float>(static_cast<int8_t>(pair[c] & 0xFFu)) * factor * sm.x;
-    float w1 = static_cast<float>(static_cast<int8_t>(pair[c] >> 8)) * factor * sm.y;
+    w0 = static_cast<float>(static_cast<int8_t>(pair[c] & 0xFFu)) * factor * sm.x;
+    w1 = static_cast<float>(static_cast<int8_t>(pair[c] >> 8)) * factor * sm.y;
     if constexpr (kMerged) {
       const float2 merge = *reinterpret_cast<const float2*>(a.record_merge + state * kTile + v * kDim + k0);
       w0 = w0 + merge.x;
@@ -202,8 +208,33 @@ __global__ __launch_bounds__(kThreads) void quant_only_refit_kernel(RefitArgs a)
         w1 = key1[j] * scalar[j] + w1;
       }
     }
-    m0[c] = w0 / sm.x;
-    m1[c] = w1 / sm.y;
+  };
+  const float y0 = 1.0f / sm.x, y1 = 1.0f / sm.y;
+  uint32_t min_key = 0xFFFFFFFFu;
+  float max_abs = 0.0f;
+  float m0[kColumnsPerWave], m1[kColumnsPerWave];
+#pragma unroll
+  for (int c = 0; c < kColumnsPerWave; ++c) {
+    float w0, w1;
+    boundary_value(c, w0, w1);
+    min_key = min(min_key, min((__float_as_uint(w0) << 1) - 1u, (__float_as_uint(w1) << 1) - 1u));
+    max_abs = fmaxf(max_abs, fmaxf(fabsf(w0), fabsf(w1)));
+    m0[c] = div_by_reciprocal(w0, sm.x, y0);
+    m1[c] = div_by_reciprocal(w1, sm.y, y1);
+  }
+  const float min_abs =
+      min_key == 0xFFFFFFFFu ? INFINITY : __uint_as_float((min_key + 1u) >> 1);
+  const bool lane_fast = min_abs >= 0x1p-100f && max_abs <= 0x1p100f &&
+                         sm.x >= 0x1p-20f && sm.x <= 0x1p20f &&
+                         sm.y >= 0x1p-20f && sm.y <= 0x1p20f;
+  if (!__all(lane_fast)) {
+#pragma unroll
+    for (int c = 0; c < kColumnsPerWave; ++c) {
+      float w0, w1;
+      boundary_value(c, w0, w1);
+      m0[c] = w0 / sm.x;
+      m1[c] = w1 / sm.y;
+    }
   }
 
   // Column maxima (scale'), then every column's multiplier 127 / scale' in one
