@@ -187,3 +187,28 @@ def test_power_refit_full_batch(device):
     assert_same(_subset(got_out, waiting), _subset(out, waiting), OUT_NAMES)
     assert_same(_subset(got_buf, waiting), _subset(buf, waiting), buf.keys())
     assert (got_ws[waiting] == 7.0).all()
+
+
+def test_quant_only_refit_outside_the_fast_division_domain(device):
+    """States whose smoothing lies outside [2^-20, 2^20], or whose boundary
+    values reach the subnormal range, take the IEEE division; they must be as
+    bit-exact as the others.  Sixteen states share each wavefront pattern."""
+    states = 64
+    print(f"quant-only refit, extreme smoothing, states={states}", flush=True)
+    buf = WG.window_buffers(states, 83, VK, positions=16)
+    buf["smoothing"][0:16] *= np.float32(2.0 ** -30)    # s below the fast domain
+    buf["smoothing"][16:32] *= np.float32(2.0 ** 30)    # s above it
+    buf["smoothing"][32:48] *= np.float32(2.0 ** -60)   # w/s products near underflow
+    buf["residual"][48] = 0                              # w = records only
+    buf["smoothing"][49, ::2] = np.float32(2.0 ** -40)   # mixed lanes in one state
+    buf["smoothing"][49, 1::2] = np.float32(2.0 ** 40)
+    out = sentinel_outputs(states)
+    d, do = to_device(buf, device), to_device(out, device)
+    workspace = torch.zeros(16, dtype=torch.float32, device=device)
+    assert native().window_boundary_launch_v1(
+        stream(), *window_ptrs(d), *out_ptrs(do), workspace.data_ptr(), states, 0) == 0
+    torch.cuda.synchronize()
+    ref, ref_out = WG.copy_buffers(buf), WG.copy_buffers(out)
+    W.window_boundary_quant_only(ref, ref_out)
+    assert_same(from_device(do, out), ref_out, OUT_NAMES)
+    assert_same(from_device(d, buf), ref, buf.keys())
