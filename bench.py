@@ -742,9 +742,9 @@ def main() -> int:
                         help="a few launches of every kernel, for rocprofv3 counter passes")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(every head tile is independent; see DESIGN.md for the sharding plan).",
-              file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (every head "
+              "tile is independent, so ranks would take contiguous tile ranges with no "
+              "exchange).", file=sys.stderr)
         return 2
 
     import torch
