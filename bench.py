@@ -8,9 +8,10 @@ rotating over 5 distinct state copies so the 256 MB Infinity Cache cannot hold
 the working set.  Kernel durations come from HIP events recorded on the stream
 the kernels are launched on (torch's current stream).  The windowed decode
 step, its window-boundary refit, the capsule wire format (serialize /
-restore) and, with --pool, config 5 are reported beside the headline line.
+restore) and config 5 (the slot-indexed fp32 and bf16 pools) are reported
+beside the headline line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--pool]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-pool]
 
 Prints one JSON line (rank 0).
 """
@@ -42,6 +43,8 @@ C3_BYTES = 256 * 32 * 128 * 128 + 2 * 256 * 32 * 128 * 4 + 256 * 16 * 128 * 2 + 
 C4_BYTES = 64 * 32 * 128 * 128 + 2 * 64 * 32 * 128 * 4 + 64 * 64 * 32 * 128 * 2 + 64 * 64 * 32 * 128 * 4
 C4_FLOPS = 2 * 64 * 64 * 32 * 128 * 128
 ROTATIONS = 5
+PROBE_TILES = 65536
+PROBE_TILE_BYTES = PROBE_TILES * (128 * 128 * 4 + 128 * 128)
 
 
 def _log(msg: str) -> None:
@@ -110,13 +113,19 @@ def _probe_library():
         getattr(lib, name).restype = ctypes.c_int32
     lib.gdn_hbm_probe_write.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint64, ctypes.c_uint32]
     lib.gdn_hbm_probe_write.restype = ctypes.c_int32
+    for name in ("gdn_hbm_probe_expand", "gdn_hbm_probe_contract"):
+        getattr(lib, name).argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint64, ctypes.c_uint32]
+        getattr(lib, name).restype = ctypes.c_int32
     lib.gdn_hbm_probe_grid.restype = ctypes.c_uint32
     return lib
 
 
 def bench_hbm_probe(repeats: int = 5):
     """Sustained HBM bandwidth of plain streaming kernels (4 GiB buffers), with
-    plain accesses and with the nontemporal hint the codec kernels use."""
+    plain accesses and with the nontemporal hint the codec kernels use: copy,
+    read, write, and the codec-shaped mixed streams expand (1:4 read:write, a
+    16 KiB byte tile in and a 64 KiB fp32 tile out per workgroup, the
+    dequantize's mix) and contract (4:1, the quantize's mix)."""
     import torch
 
     lib = _probe_library()
@@ -134,6 +143,11 @@ def bench_hbm_probe(repeats: int = 5):
             "read": (lambda: lib.gdn_hbm_probe_read(stream, src.data_ptr(), sink.data_ptr(), nbytes,
                                                     mode), nbytes),
             "write": (lambda: lib.gdn_hbm_probe_write(stream, dst.data_ptr(), nbytes, mode), nbytes),
+            # 65,536 tiles: 1 GiB of bytes <-> 4 GiB of fp32.
+            "expand": (lambda: lib.gdn_hbm_probe_expand(stream, src.data_ptr(), dst.data_ptr(),
+                                                        PROBE_TILES, mode), PROBE_TILE_BYTES),
+            "contract": (lambda: lib.gdn_hbm_probe_contract(stream, src.data_ptr(), dst.data_ptr(),
+                                                            PROBE_TILES, mode), PROBE_TILE_BYTES),
         }
         for name, (fn, moved) in launches.items():
             for _ in range(2):
@@ -192,7 +206,7 @@ def bench_decode_projection(steps: int, warmup: int):
     b.record()
     us = _events_ms([(a, b)])[0] / n * 1e3
     _log(f"config 3: decode projection {us:.2f} us/step")
-    return us
+    return us, sets[0]
 
 
 def bench_chunked_projection(steps: int, warmup: int):
@@ -223,7 +237,101 @@ def bench_chunked_projection(steps: int, warmup: int):
     b.record()
     us = _events_ms([(a, b)])[0] / n * 1e3
     _log(f"config 4: chunked projection {us:.2f} us/step")
-    return us
+    return us, sets[0]
+
+
+def cpu_baseline_projection(sample, chunked: bool, gpu_us: float, target_seconds: float = 6.0):
+    """The reference's own CPU readout (oracle/_ref: ReadWindowState with an
+    empty window, state_capsule.cpp:253-306) over the whole config-3 step
+    (8,192 heads) or config-4 step (2,048 heads x 64 tokens), on identical
+    input bits: the [value][key] codes transposed to the reference's [key][value]
+    layout and the bf16 queries widened to fp32 (query scale 1) before timing.
+    One thread over the whole step, then every allowed core with the heads
+    split contiguously, repeated to about `target_seconds`.  The CPU outputs of
+    the first 256 heads are checked against the GPU's within the fp32 bound
+    2^-14 * sum|terms| (each side lies within 2^-15 of the exact value)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    import torch
+
+    import oracle
+
+    if not oracle.ref_available():
+        return None
+    codes_d, smoothing_d, scales_d, queries_d, out_d = sample
+    torch.cuda.synchronize()
+    codes_vk = codes_d.cpu().numpy()
+    seqs, heads = codes_vk.shape[:2]
+    codes = np.ascontiguousarray(codes_vk.swapaxes(-1, -2)).reshape(-1, 128, 128)
+    smoothing = smoothing_d.cpu().numpy().reshape(-1, 128)
+    scales = scales_d.cpu().numpy().reshape(-1, 128)
+    q_bits = queries_d.view(torch.int16).cpu().numpy().view(np.uint16)
+    gpu_out = out_d.cpu().numpy()
+    if chunked:  # q [N,T,Hq,128] -> reads [N*H, T, 128]
+        group = heads // q_bits.shape[2]
+        q = np.repeat(q_bits, group, axis=2).transpose(0, 2, 1, 3)
+        reads = oracle.bf16_to_f32(q).reshape(seqs * heads, -1, 128)
+        gpu = gpu_out.transpose(0, 2, 1, 3).reshape(seqs * heads, -1, 128)
+    else:  # q [B,Hq,128] -> reads [B*H, 1, 128]
+        group = heads // q_bits.shape[1]
+        reads = oracle.bf16_to_f32(np.repeat(q_bits, group, axis=1)).reshape(-1, 1, 128)
+        gpu = gpu_out.reshape(-1, 1, 128)
+    reads = np.ascontiguousarray(reads, np.float32)
+    total = codes.shape[0]
+
+    def run(lo, hi):
+        return oracle.ref_read_boundary_heads(codes[lo:hi], smoothing[lo:hi], scales[lo:hi],
+                                              reads[lo:hi])
+
+    t0 = time.perf_counter()
+    cpu_out = run(0, total)
+    single = time.perf_counter() - t0
+    threads = _cpu_threads()
+    bounds = np.linspace(0, total, threads + 1).astype(int)
+    reps = max(1, int(target_seconds * threads / max(single, 1e-6) / 2))
+    reps = min(reps, 50)
+
+    def part(i):
+        for _ in range(reps):
+            run(bounds[i], bounds[i + 1])
+
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(threads) as pool:
+        list(pool.map(part, range(threads)))
+    multi = (time.perf_counter() - t0) / reps
+    # Parity on the first 256 heads against the oracle's exact value and bound.
+    n = min(256, total)
+    if chunked:
+        idx_q = q_bits.reshape(seqs, q_bits.shape[1], q_bits.shape[2], 128)
+        sub = n // heads or 1
+        _, exact, bound = oracle.project_chunked(codes_vk[:sub], smoothing_d.cpu().numpy()[:sub],
+                                                 scales_d.cpu().numpy()[:sub], idx_q[:sub], 1.0,
+                                                 oracle.LAYOUT_VALUE_KEY, threads=threads)
+        exact = exact.transpose(0, 2, 1, 3).reshape(sub * heads, -1, 128)
+        bound = bound.transpose(0, 2, 1, 3).reshape(sub * heads, -1, 128)
+        n = sub * heads
+    else:
+        sub = n // heads or 1
+        _, exact, bound = oracle.project_decode(codes_vk[:sub], smoothing_d.cpu().numpy()[:sub],
+                                                scales_d.cpu().numpy()[:sub], q_bits[:sub], 1.0,
+                                                oracle.LAYOUT_VALUE_KEY)
+        exact, bound = exact.reshape(-1, 1, 128), bound.reshape(-1, 1, 128)
+        n = sub * heads
+    within = bool((np.abs(cpu_out[:n] - gpu[:n]) <= 2.0 ** -14 * bound + 1e-30).all()
+                  and (np.abs(cpu_out[:n] - exact) <= 2.0 ** -15 * bound + 1e-30).all())
+    name = "config 4" if chunked else "config 3"
+    _log(f"cpu baseline {name} (reference): {single * 1e6:.0f} us/step on 1 thread, "
+         f"{multi * 1e6:.0f} us/step on {threads} threads; GPU within bound={within}")
+    step = (f"{total} heads x {reads.shape[1]} tokens" if chunked else f"{total} heads")
+    return {"value": multi * 1e6, "unit": "us/step", "cores": threads, "kind": "reference",
+            "cpu_model": _cpu_model(),
+            "sample": f"the whole step ({step}), the reference's ReadWindowState per read, "
+                      f"heads split contiguously over {threads} threads, {reps} passes",
+            "gpu_speedup": multi * 1e6 / gpu_us,
+            "single_thread": {"value": single * 1e6, "unit": "us/step", "cores": 1,
+                              "sample": "one pass over the whole step"},
+            "gpu_within_fp32_bound_on_first_heads": within}
 
 
 WINDOW_STATES = 256 * 32  # B = 256 sequences x 32 value heads
@@ -571,24 +679,42 @@ def cpu_baseline_capsule(target_seconds: float = 8.0):
                           "single_thread": {**rates(ser_1, states), "cores": 1}},
             "restore": {**rates(res_n, states * reps), "cores": threads,
                         "single_thread": {**rates(res_1, states), "cores": 1}},
-            "kind": "port",
+            "kind": "port", "cpu_model": _cpu_model(),
             "sample": f"the whole {states}-capsule bench batch ({nbytes} capsule bytes), "
                       f"{reps} passes with the states dealt round-robin to {threads} threads; "
                       f"one pass on 1 thread",
             "gpu_capsules_byte_identical": bool(ok)}
 
 
-def bench_pool(steps: int, warmup: int):
-    """Config 5 with a bf16 pool (64.4 GB): gather-encode and decode-scatter."""
+POOL_LAYERS, POOL_SLOTS, POOL_HEADS, POOL_BATCH, POOL_PADDING = 30, 2048, 32, 512, 26
+
+
+def pool_bytes_per_direction(dtype_bytes: int) -> int:
+    """Algorithmic bytes of one config-5 direction: per valid (layer, slot,
+    head) tile the pool tile (fp32 65,536 B or bf16 32,768 B), the int8 codes
+    (16,384 B) and the fp32 smoothing and scales (1,024 B)."""
+    per_head = 128 * 128 * dtype_bytes + 128 * 128 + 2 * 128 * 4
+    return (POOL_BATCH - POOL_PADDING) * POOL_LAYERS * POOL_HEADS * per_head
+
+
+def bench_pool(steps: int, warmup: int, dtype_name: str):
+    """Config 5: a [30 layers][2048 slots][32 heads][128][128] state pool in
+    the provider's [value][key] layout (fp32 128.8 GB or bf16 64.4 GB),
+    Student-t(3) x 0.05 entries with 2% all-zero heads, a batch of 512 random
+    unique slot ids of which 26 are padding (-1).  Gather-encode (pool ->
+    compact codes) and decode-scatter (codes -> pool) are timed separately,
+    each launch between its own HIP events."""
     import torch
 
     from gdn_state_codec import codec
 
     dev = torch.device("cuda:0")
+    dtype = torch.float32 if dtype_name == "f32" else torch.bfloat16
     gen = torch.Generator(device=dev)
     gen.manual_seed(5)
-    layers, slots, heads, batch = 30, 2048, 32, 512
-    pool = torch.empty((layers, slots, heads, 128, 128), dtype=torch.bfloat16, device=dev)
+    layers, slots, heads, batch = POOL_LAYERS, POOL_SLOTS, POOL_HEADS, POOL_BATCH
+    _log(f"config 5: generating a {dtype_name} pool {layers}x{slots}x{heads}x128x128")
+    pool = torch.empty((layers, slots, heads, 128, 128), dtype=dtype, device=dev)
     for layer in range(layers):
         # Student-t(3) = Z / sqrt(chi2_3 / 3), chi2_3 a sum of three squared normals.
         for part in range(0, slots, 256):
@@ -597,37 +723,58 @@ def bench_pool(steps: int, warmup: int):
             chi = torch.zeros(shape, device=dev)
             for _ in range(3):
                 chi.addcmul_(w := torch.randn(shape, generator=gen, device=dev), w)
-            pool[layer, part:part + shape[0]] = (z * torch.rsqrt(chi / 3) * 0.05).to(torch.bfloat16)
+            pool[layer, part:part + shape[0]] = (z * torch.rsqrt(chi / 3) * 0.05).to(dtype)
             del z, chi, w
     zero = torch.rand((layers, slots, heads), generator=gen, device=dev) < 0.02
     pool[zero] = 0
+    del zero
     perm = torch.randperm(slots, generator=gen, device=dev)[:batch].to(torch.int32)
-    pad = torch.randperm(batch, generator=gen, device=dev)[:26]
+    pad = torch.randperm(batch, generator=gen, device=dev)[:POOL_PADDING]
     perm[pad] = -1
-    codes, s, sc = codec.pool_encode(pool, perm)
+    layout = codec.LAYOUT_VALUE_KEY
+    codes, s, sc = codec.pool_encode(pool, perm, layout)
     for _ in range(warmup):
-        codec.pool_encode(pool, perm, codec.LAYOUT_KEY_VALUE, codes, s, sc)
-        codec.pool_decode(codes, s, sc, perm, pool)
+        codec.pool_encode(pool, perm, layout, codes, s, sc)
+        codec.pool_decode(codes, s, sc, perm, pool, layout)
     enc, dec = [], []
     for _ in range(steps):
         e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
         e0.record()
-        codec.pool_encode(pool, perm, codec.LAYOUT_KEY_VALUE, codes, s, sc)
+        codec.pool_encode(pool, perm, layout, codes, s, sc)
         e1.record()
-        codec.pool_decode(codes, s, sc, perm, pool)
+        codec.pool_decode(codes, s, sc, perm, pool, layout)
         e2.record()
         enc.append((e0, e1))
         dec.append((e1, e2))
     enc_ms = sum(_events_ms(enc)) / steps
     dec_ms = sum(_events_ms(dec)) / steps
-    valid = batch - 26
-    per_head = 128 * 128 * 2 + 128 * 128 + 2 * 128 * 4
-    nbytes = valid * layers * heads * per_head
-    del pool, codes
-    return {"encode_ms": enc_ms, "decode_ms": dec_ms,
-            "encode_GBps": nbytes / (enc_ms * 1e-3) / 1e9,
-            "decode_GBps": nbytes / (dec_ms * 1e-3) / 1e9,
-            "bytes_per_direction": nbytes, "pool_dtype": "bf16"}
+    nbytes = pool_bytes_per_direction(4 if dtype_name == "f32" else 2)
+    del pool, codes, s, sc
+    torch.cuda.empty_cache()
+    result = {"encode_ms": enc_ms, "decode_ms": dec_ms,
+              "encode_GBps": nbytes / (enc_ms * 1e-3) / 1e9,
+              "decode_GBps": nbytes / (dec_ms * 1e-3) / 1e9,
+              "encode_hbm_frac": nbytes / (enc_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+              "decode_hbm_frac": nbytes / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+              "bytes_per_direction": nbytes, "pool_dtype": dtype_name, "layout": "[value][key]",
+              "valid_slots": batch - POOL_PADDING, "steps": steps}
+    _log(f"config 5 ({dtype_name} pool): gather-encode {enc_ms:.3f} ms "
+         f"({result['encode_GBps']:.0f} GB/s), decode-scatter {dec_ms:.3f} ms "
+         f"({result['decode_GBps']:.0f} GB/s)")
+    return result
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for every cpu_baseline."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
 
 
 def _cpu_threads() -> int:
@@ -694,6 +841,7 @@ def cpu_baseline(state, codes, smoothing, scales, target_seconds: float = 8.0):
     _log(f"cpu baseline ({kind}): {m} heads in {m_seconds:.1f} s on {threads} threads -> "
          f"{multi:.3f} GB/s")
     return {"value": multi, "unit": "GB/s", "cores": threads, "kind": kind,
+            "cpu_model": _cpu_model(),
             "sample": f"{m} heads (the first {m} of the config-2 state), quantize+dequantize, "
                       f"heads split contiguously over {threads} threads",
             "seconds": m_seconds,
@@ -702,14 +850,31 @@ def cpu_baseline(state, codes, smoothing, scales, target_seconds: float = 8.0):
             "gpu_codes_bit_exact_on_sample": bool(parity and same)}
 
 
-def _traffic():
-    path = ROOT / "profiles" / "encode_c2_traffic.json"
+def _traffic(kernel: str):
+    """HBM bytes per launch of `kernel` at config 2, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary committed under profiles/."""
+    path = ROOT / "profiles" / f"{kernel}_c2_traffic.json"
     if not path.is_file():
         return None
     try:
         return json.loads(path.read_text()).get("bytes_per_launch")
     except (ValueError, OSError):
         return None
+
+
+def codec_roofline(enc_ms: float, dec_ms: float) -> dict:
+    """The roofline object of the config-2 codec: the slower (dominant) of the
+    two kernels at the top level, both under "kernels"."""
+    kernels = {}
+    for name, label, ms in (("decode_kernel", "dequantize", dec_ms),
+                            ("encode_kernel", "quantize", enc_ms)):
+        achieved = C2_BYTES / (ms * 1e-3) / 1e9
+        kernels[name] = {"kernel": f"{name} ({label})", "bound": "hbm", "achieved": achieved,
+                         "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
+                         "traffic": _traffic(name), "algorithmic_bytes_per_launch": C2_BYTES,
+                         "ms": ms}
+    dominant = "decode_kernel" if dec_ms >= enc_ms else "encode_kernel"
+    return {**kernels[dominant], "dominant": True, "kernels": kernels}
 
 
 def profile_pass() -> int:
@@ -725,6 +890,9 @@ def profile_pass() -> int:
     bench_window_step(0)
     bench_refit(1, 0)
     bench_capsule(1, 0)
+    torch.cuda.empty_cache()
+    bench_pool(1, 0, "f32")
+    bench_pool(1, 0, "bf16")
     torch.cuda.synchronize()
     print(json.dumps({"profile_pass": "done"}), flush=True)
     return 0
@@ -736,7 +904,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    parser.add_argument("--pool", action="store_true", help="also run config 5 (bf16 pool)")
+    parser.add_argument("--no-pool", action="store_true",
+                        help="skip config 5 (the fp32 and bf16 slot pools)")
     parser.add_argument("--only-codec", action="store_true", help="config 2 only")
     parser.add_argument("--profile", action="store_true",
                         help="a few launches of every kernel, for rocprofv3 counter passes")
@@ -767,13 +936,18 @@ def main() -> int:
     extra = {}
     if not args.only_codec:
         extra["hbm_probe"] = bench_hbm_probe()
-        dec_us = bench_decode_projection(args.steps, args.warmup)
-        chunk_us = bench_chunked_projection(args.steps, args.warmup)
+        dec_us, dec_sample = bench_decode_projection(args.steps, args.warmup)
         extra["decode_projection"] = {
             "workload": "config 3: B=256, 32 value heads (GQA from 16), int8 [256,32,128,128]",
             "us_per_step": dec_us, "GBps": C3_BYTES / (dec_us * 1e-6) / 1e9,
             "hbm_frac": C3_BYTES / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
             "bytes_per_step": C3_BYTES, "rotated_state_copies": ROTATIONS}
+        if not args.no_cpu:
+            extra["decode_projection"]["cpu_baseline"] = cpu_baseline_projection(
+                dec_sample, False, dec_us)
+        del dec_sample
+        torch.cuda.empty_cache()
+        chunk_us, chunk_sample = bench_chunked_projection(args.steps, args.warmup)
         extra["chunked_projection"] = {
             "workload": "config 4: 64 seqs x T=64 x 32 heads, bf16 MFMA",
             "us_per_step": chunk_us, "GBps": C4_BYTES / (chunk_us * 1e-6) / 1e9,
@@ -781,6 +955,10 @@ def main() -> int:
             "TFLOPs": C4_FLOPS / (chunk_us * 1e-6) / 1e12,
             "mfma_frac_of_useful_flops": C4_FLOPS / (chunk_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
             "bytes_per_step": C4_BYTES, "rotated_state_copies": ROTATIONS}
+        if not args.no_cpu:
+            extra["chunked_projection"]["cpu_baseline"] = cpu_baseline_projection(
+                chunk_sample, True, chunk_us)
+        del chunk_sample
         torch.cuda.empty_cache()
         extra["windowed_step"] = bench_window_step(args.warmup)
         torch.cuda.empty_cache()
@@ -789,8 +967,13 @@ def main() -> int:
         extra["capsule"] = bench_capsule(max(args.steps // 4, 3), args.warmup)
         if not args.no_cpu:
             extra["capsule"]["cpu_baseline"] = cpu_baseline_capsule()
-    if args.pool:
-        extra["pool_codec"] = bench_pool(max(args.steps // 4, 2), 1)
+    if not args.no_pool and not args.only_codec:
+        torch.cuda.empty_cache()
+        extra["pool_codec"] = {
+            "workload": "config 5: slot-indexed pool [30][2048][32][128][128], batch 512 random "
+                        "unique slot ids with 26 padding (-1), Student-t(3) x 0.05, 2% zero heads",
+            "f32": bench_pool(max(args.steps // 4, 3), 1, "f32"),
+            "bf16": bench_pool(max(args.steps // 4, 3), 1, "bf16")}
     line = {
         "metric": METRIC,
         "value": value,
@@ -810,10 +993,7 @@ def main() -> int:
                    "tiles": C2_TILES, "bytes_per_direction": C2_BYTES},
         "quantize": {"ms": enc_ms, "GBps": enc_gbps, "hbm_frac": enc_gbps / HBM_PEAK_GBPS},
         "dequantize": {"ms": dec_ms, "GBps": dec_gbps, "hbm_frac": dec_gbps / HBM_PEAK_GBPS},
-        "roofline": {"kernel": "encode_kernel (quantize)", "bound": "hbm",
-                     "achieved": enc_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": enc_gbps / HBM_PEAK_GBPS, "traffic": _traffic(),
-                     "algorithmic_bytes_per_launch": C2_BYTES},
+        "roofline": codec_roofline(enc_ms, dec_ms),
         "cpu_baseline": cpu,
         **extra,
     }

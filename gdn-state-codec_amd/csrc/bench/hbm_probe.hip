@@ -1,6 +1,6 @@
 // HBM bandwidth probes used by bench.py (not part of the codec's C-ABI).
 //
-// Three streaming kernels with the codec's access granularity (16-byte
+// Streaming kernels with the codec's access granularity (16-byte
 // vector loads/stores, 256-thread workgroups, one contiguous 4 KiB chunk per
 // workgroup iteration): copy, read-only and write-only, each with plain and
 // with nontemporal accesses (the hint the codec kernels use).  They give the
@@ -94,6 +94,73 @@ __global__ __launch_bounds__(kThreads) void write_kernel(uint4* __restrict__ dst
   }
 }
 
+// Tile-shaped mixed streams with the codec's exact access pattern, one
+// 256-thread workgroup per 128 x 128 tile: thread t touches rows
+// 8j + t / 32 (j = 0..15), four consecutive columns 4 (t % 32)..+3 of each.
+//   expand   (1:4 read:write, the dequantize's mix): 16 KiB of bytes in, each
+//            byte widened to an fp32 value, 64 KiB out; a 4-byte load and a
+//            16-byte store per row.
+//   contract (4:1, the quantize's mix): 64 KiB of fp32 in, each value's low
+//            byte kept, 16 KiB out; a 16-byte load and a 4-byte store per row.
+// Loads are all issued before the stores, as in the codec kernels.
+constexpr int kTileDim = 128;
+constexpr int kRowsPerThread = 16;
+
+template <bool kNontemporal>
+__global__ __launch_bounds__(kThreads) void expand_kernel(const uint32_t* __restrict__ src,
+                                                          float4* __restrict__ dst) {
+  const uint64_t tile = blockIdx.x;
+  const int row0 = threadIdx.x >> 5;
+  const int quad = threadIdx.x & 31;
+  const uint32_t* in = src + tile * (kTileDim * kTileDim / 4);
+  float4* out = dst + tile * (kTileDim * kTileDim / 4);
+  uint32_t w[kRowsPerThread];
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const uint32_t* p = in + (8 * j + row0) * (kTileDim / 4) + quad;
+    w[j] = kNontemporal ? __builtin_nontemporal_load(p) : *p;
+  }
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const float4 v = make_float4(static_cast<float>(w[j] & 0xFFu),
+                                 static_cast<float>((w[j] >> 8) & 0xFFu),
+                                 static_cast<float>((w[j] >> 16) & 0xFFu),
+                                 static_cast<float>(w[j] >> 24));
+    float4* q = out + (8 * j + row0) * (kTileDim / 4) + quad;
+    if (kNontemporal) {
+      gdn::stream_store(q, v);
+    } else {
+      *q = v;
+    }
+  }
+}
+
+template <bool kNontemporal>
+__global__ __launch_bounds__(kThreads) void contract_kernel(const uint4* __restrict__ src,
+                                                            uint32_t* __restrict__ dst) {
+  const uint64_t tile = blockIdx.x;
+  const int row0 = threadIdx.x >> 5;
+  const int quad = threadIdx.x & 31;
+  const uint4* in = src + tile * (kTileDim * kTileDim / 4);
+  uint32_t* out = dst + tile * (kTileDim * kTileDim / 4);
+  uint4 v[kRowsPerThread];
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    v[j] = load16<kNontemporal>(in + (8 * j + row0) * (kTileDim / 4) + quad);
+  }
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const uint32_t packed = (v[j].x & 0xFFu) | ((v[j].y & 0xFFu) << 8) |
+                            ((v[j].z & 0xFFu) << 16) | (v[j].w << 24);
+    uint32_t* q = out + (8 * j + row0) * (kTileDim / 4) + quad;
+    if (kNontemporal) {
+      __builtin_nontemporal_store(packed, q);
+    } else {
+      *q = packed;
+    }
+  }
+}
+
 }  // namespace
 
 // Grid size used by every probe: enough workgroups to fill 256 CUs many
@@ -130,5 +197,33 @@ extern "C" int32_t gdn_hbm_probe_write(void* stream, void* dst, uint64_t bytes,
   hipLaunchKernelGGL(kernel, dim3(gdn_hbm_probe_grid()), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<uint4*>(dst),
                      bytes / 16, 0x3F800000u);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+// 1:4 stream: `tiles` 16 KiB tiles of bytes at src widened into `tiles`
+// 64 KiB tiles of fp32 at dst (one workgroup per tile).
+extern "C" int32_t gdn_hbm_probe_expand(void* stream, const void* src, void* dst,
+                                        uint64_t tiles, uint32_t mode) {
+  if (src == nullptr || dst == nullptr || tiles == 0 || tiles > 0x7FFFFFFFull || mode > 1) {
+    return 1;
+  }
+  const auto kernel = mode ? expand_kernel<true> : expand_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint32_t*>(src),
+                     static_cast<float4*>(dst));
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+// 4:1 stream: `tiles` 64 KiB tiles at src narrowed into `tiles` 16 KiB tiles
+// at dst (one workgroup per tile).
+extern "C" int32_t gdn_hbm_probe_contract(void* stream, const void* src, void* dst,
+                                          uint64_t tiles, uint32_t mode) {
+  if (src == nullptr || dst == nullptr || tiles == 0 || tiles > 0x7FFFFFFFull || mode > 1) {
+    return 1;
+  }
+  const auto kernel = mode ? contract_kernel<true> : contract_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint4*>(src),
+                     static_cast<uint32_t*>(dst));
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }

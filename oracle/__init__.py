@@ -83,6 +83,8 @@ def lib() -> ctypes.CDLL:
         l.gdn_oracle_pool_decode.restype = None
         l.gdn_oracle_f32_to_bf16.argtypes = [_F]
         l.gdn_oracle_f32_to_bf16.restype = ctypes.c_uint16
+        l.gdn_oracle_f32_to_bf16_array.argtypes = [_P, _U64, _P]
+        l.gdn_oracle_f32_to_bf16_array.restype = None
         _lib = l
     return _lib
 
@@ -112,6 +114,8 @@ def ref() -> ctypes.CDLL:
         r.gdnref_quantize_heads.restype = _I
         r.gdnref_dequantize_heads.argtypes = [_P, _P, _P, _U64, _U32, _U32, _P]
         r.gdnref_dequantize_heads.restype = _I
+        r.gdnref_read_boundary_heads.argtypes = [_P, _P, _P, _U64, _U32, _U32, _U32, _P, _P]
+        r.gdnref_read_boundary_heads.restype = _I
         _ref = r
     return _ref
 
@@ -279,6 +283,14 @@ def f32_to_bf16(values: np.ndarray) -> np.ndarray:
     return ((bits + 0x7FFF + lsb) >> 16).astype(np.uint16)
 
 
+def c_f32_to_bf16(values: np.ndarray) -> np.ndarray:
+    """The C restatement's narrowing (gdn_oracle_f32_to_bf16), elementwise."""
+    values = np.ascontiguousarray(values, np.float32)
+    out = np.empty(values.shape, np.uint16)
+    lib().gdn_oracle_f32_to_bf16_array(_ptr(values), values.size, _ptr(out))
+    return out
+
+
 def bf16_to_f32(values: np.ndarray) -> np.ndarray:
     return (np.asarray(values, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
@@ -358,3 +370,19 @@ def ref_dequantize_heads(codes, smoothing, scales):
                                            DIM, _ptr(state))
     assert status == 0
     return state
+
+
+def ref_read_boundary_heads(codes, smoothing, scales, reads):
+    """The reference's ReadWindowState boundary readout: codes [N,128,128]
+    [K][V], smoothing/scales [N,128], reads fp32 [N,T,128] -> [N,T,128]."""
+    codes = np.ascontiguousarray(codes, np.int8)
+    heads = codes.size // TILE
+    reads = np.ascontiguousarray(reads, np.float32).reshape(heads, -1, DIM)
+    tokens = reads.shape[1]
+    out = np.empty((heads, tokens, DIM), np.float32)
+    status = ref().gdnref_read_boundary_heads(
+        _ptr(codes), _ptr(np.ascontiguousarray(smoothing, np.float32)),
+        _ptr(np.ascontiguousarray(scales, np.float32)), heads, tokens, DIM, DIM,
+        _ptr(reads), _ptr(out))
+    assert status == 0
+    return out

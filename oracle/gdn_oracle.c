@@ -55,6 +55,10 @@ uint16_t gdn_oracle_f32_to_bf16(float value) {
   return (uint16_t)((bits + 0x7FFFu + least_significant) >> 16);
 }
 
+void gdn_oracle_f32_to_bf16_array(const float* values, uint64_t count, uint16_t* out) {
+  for (uint64_t i = 0; i < count; ++i) out[i] = gdn_oracle_f32_to_bf16(values[i]);
+}
+
 /* ------------------------------------------------------ single head, [K][V] */
 
 void gdn_oracle_quantize_kv(const float* dense, uint32_t keys, uint32_t values,

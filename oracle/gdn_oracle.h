@@ -130,6 +130,8 @@ void gdn_oracle_pool_decode(const int8_t* codes, const float* smoothing,
  * reference's FloatToBFloat16 (windowed_gdn_step.cpp:26-32). */
 float gdn_oracle_bf16_to_f32(uint16_t value);
 uint16_t gdn_oracle_f32_to_bf16(float value);
+/* gdn_oracle_f32_to_bf16 over an array. */
+void gdn_oracle_f32_to_bf16_array(const float* values, uint64_t count, uint16_t* out);
 
 /* fp16 helpers (IEEE binary16): widening is exact; narrowing rounds to nearest
  * even with subnormals and overflow to infinity. */

@@ -285,6 +285,42 @@ int gdnref_dequantize_heads(const std::int8_t* residual,
   return 0;
 }
 
+// The boundary readout (ReadWindowState with an empty window,
+// state_capsule.cpp:253-306) of `heads` contiguous [K][V] boundaries, each
+// read with `tokens` vectors: reads [heads][tokens][K], outputs
+// [heads][tokens][V].  Each head's Boundary is built once and read `tokens`
+// times, as a capsule is between window boundaries.  bench.py's CPU baseline of
+// the encoded projection (decode: tokens = 1; chunked: tokens = T).
+int gdnref_read_boundary_heads(const std::int8_t* residual, const float* smoothing,
+                               const float* value_scales, std::uint64_t heads,
+                               std::uint32_t tokens, std::uint32_t keys,
+                               std::uint32_t values, const float* reads,
+                               float* outputs) {
+  try {
+    const auto identity = MakeIdentity(keys, values);
+    const auto parameters = MakeParameters(0);
+    const std::vector<statecentric::GdnStateCodecCapsule::UpdateRecord> none;
+    const std::size_t tile = std::size_t{keys} * values;
+    for (std::uint64_t head = 0; head < heads; ++head) {
+      statecentric::GdnStateCodecCapsule::Boundary boundary;
+      boundary.residual.assign(residual + head * tile, residual + (head + 1) * tile);
+      boundary.smoothing.assign(smoothing + head * keys, smoothing + (head + 1) * keys);
+      boundary.value_scales.assign(value_scales + head * values,
+                                   value_scales + (head + 1) * values);
+      for (std::uint32_t t = 0; t < tokens; ++t) {
+        const std::size_t row = head * tokens + t;
+        const auto out = statecentric::ReadWindowState(
+            boundary, none, std::span<const float>(reads + row * keys, keys), identity,
+            parameters);
+        std::memcpy(outputs + row * values, out.data(), values * sizeof(float));
+      }
+    }
+    return 0;
+  } catch (const std::exception&) {
+    return 1;
+  }
+}
+
 // Sha256Hex (native/src/sha256.cpp): 64 lowercase hex characters of the
 // SHA-256 of `size` bytes.
 int gdnref_sha256_hex(const std::uint8_t* data, std::uint64_t size, char* hex) {
