@@ -327,6 +327,20 @@ int32_t launch_refit(void* stream, const RefitArgs& args) {
 
 }  // namespace
 
+// The quant-only refit (records folded, existing smoothing) of `states` slot states.
+int32_t launch_quant_only_refit(void* stream, const int8_t* residual, const float* smoothing,
+                                const float* scales, float* record_decay,
+                                uint16_t* record_keys, uint16_t* record_corrections,
+                                uint32_t* positions, int8_t* next_residual,
+                                float* next_smoothing, float* next_scales,
+                                uint16_t* next_comp_keys, uint16_t* next_comp_values,
+                                uint32_t states) {
+  const RefitArgs args{residual, smoothing, scales, record_decay, record_keys,
+                       record_corrections, positions, next_residual, next_smoothing,
+                       next_scales, next_comp_keys, next_comp_values, nullptr, states};
+  return launch_refit(stream, args);
+}
+
 int32_t launch_power_refit(void* stream, const int8_t* residual, const float* smoothing,
                            const float* scales, const uint16_t* comp_keys,
                            const uint16_t* comp_values, float* record_decay,
@@ -371,11 +385,10 @@ extern "C" int32_t statecentric_gdn_state_codec_window_boundary_launch_v1(
                                    next_scales, next_compensator_keys, next_compensator_values,
                                    residual_workspace, states, power_iterations);
   }
-  const gdn::RefitArgs args{residual, smoothing, scales, record_decay, record_keys,
-                            record_corrections, positions, next_residual, next_smoothing,
-                            next_scales, next_compensator_keys, next_compensator_values,
-                            nullptr, states};
-  return gdn::launch_refit(stream, args);
+  return gdn::launch_quant_only_refit(stream, residual, smoothing, scales, record_decay,
+                                      record_keys, record_corrections, positions, next_residual,
+                                      next_smoothing, next_scales, next_compensator_keys,
+                                      next_compensator_values, states);
 }
 
 extern "C" int32_t statecentric_gdn_state_codec_window_boundary_cube_finish_launch_v1(

@@ -23,6 +23,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "codec_math.h"
 #include "gdn_state_codec_window.h"
 #include "launch.h"
@@ -335,6 +337,41 @@ __global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
   if (t == 0) a.positions[state * kPositionStride] = 0u;
 }
 
+// The residual workspace of the allocation-free refit entry point: room for
+// kNoAllocMaxStates states (32 MiB), one copy per GPU, held by every GPU this
+// library runs on until the process ends.  In host code `scratch` names a
+// host-side stand-in, never the device array: host code uses only the address
+// hipGetSymbolAddress returns for the GPU in question (scratch_on_device).
+constexpr uint32_t kNoAllocMaxStates = 512;
+static __device__ __align__(256) float scratch[kNoAllocMaxStates * kTile];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+float* scratch_address[kMaxDevices] = {};
+
+// The device address of `scratch` on the GPU that `stream` runs on, looked up
+// once per GPU with that GPU current (and the caller's current GPU restored).
+int32_t scratch_on_device(void* stream, float** address) {
+  int device = 0;
+  if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &device) != hipSuccess ||
+      device < 0 || device >= kMaxDevices) {
+    return kStatusLaunchFailed;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_address[device] == nullptr) {
+    int current = 0;
+    if (hipGetDevice(&current) != hipSuccess) return kStatusLaunchFailed;
+    if (current != device && hipSetDevice(device) != hipSuccess) return kStatusLaunchFailed;
+    void* found = nullptr;
+    const hipError_t status = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+    if (current != device && hipSetDevice(current) != hipSuccess) return kStatusLaunchFailed;
+    if (status != hipSuccess || found == nullptr) return kStatusLaunchFailed;
+    scratch_address[device] = static_cast<float*>(found);
+  }
+  *address = scratch_address[device];
+  return kStatusOk;
+}
+
 }  // namespace
 
 int32_t launch_power_refit(void* stream, const int8_t* residual, const float* smoothing,
@@ -357,4 +394,45 @@ int32_t launch_power_refit(void* stream, const int8_t* residual, const float* sm
   return status == hipSuccess ? kStatusOk : kStatusLaunchFailed;
 }
 
+int32_t launch_quant_only_refit(void* stream, const int8_t* residual, const float* smoothing,
+                                const float* scales, float* record_decay,
+                                uint16_t* record_keys, uint16_t* record_corrections,
+                                uint32_t* positions, int8_t* next_residual,
+                                float* next_smoothing, float* next_scales,
+                                uint16_t* next_comp_keys, uint16_t* next_comp_values,
+                                uint32_t states);
+
 }  // namespace gdn
+
+// The window-boundary refit without a caller workspace: the power refit's
+// fitted residual goes to the library's own scratch array, so the call
+// allocates nothing.  Calls that overlap on one GPU share that array and race.
+extern "C" int32_t statecentric_gdn_state_codec_window_boundary_noalloc_launch_v1(
+    void* stream, const int8_t* residual, const float* smoothing, const float* scales,
+    const uint16_t* compensator_keys, const uint16_t* compensator_values,
+    float* record_decay, uint16_t* record_keys, uint16_t* record_corrections,
+    uint32_t* positions, int8_t* next_residual, float* next_smoothing, float* next_scales,
+    uint16_t* next_compensator_keys, uint16_t* next_compensator_values, uint32_t states,
+    uint32_t power_iterations) {
+  if (!residual || !smoothing || !scales || !compensator_keys || !compensator_values ||
+      !record_decay || !record_keys || !record_corrections || !positions || !next_residual ||
+      !next_smoothing || !next_scales || !next_compensator_keys || !next_compensator_values ||
+      states == 0 || states > gdn::kMaxWindowStates || power_iterations > 32 ||
+      (power_iterations > 0 && states > gdn::kNoAllocMaxStates)) {
+    return gdn::kStatusInvalidArgument;
+  }
+  if (power_iterations == 0) {  // the quant-only refit uses no workspace
+    return gdn::launch_quant_only_refit(stream, residual, smoothing, scales, record_decay,
+                                        record_keys, record_corrections, positions,
+                                        next_residual, next_smoothing, next_scales,
+                                        next_compensator_keys, next_compensator_values, states);
+  }
+  float* workspace = nullptr;
+  const int32_t found = gdn::scratch_on_device(stream, &workspace);
+  if (found != gdn::kStatusOk) return found;
+  return gdn::launch_power_refit(stream, residual, smoothing, scales, compensator_keys,
+                                 compensator_values, record_decay, record_keys,
+                                 record_corrections, positions, next_residual, next_smoothing,
+                                 next_scales, next_compensator_keys, next_compensator_values,
+                                 workspace, states, power_iterations);
+}

@@ -59,6 +59,7 @@ SIGNATURES: dict[str, list] = {
     "statecentric_gdn_state_codec_decode_runtime_step_v1": [_P] * 17 + [_U32],
     # window-boundary refit
     "statecentric_gdn_state_codec_window_boundary_launch_v1": [_P] * 16 + [_U32, _U32],
+    "statecentric_gdn_state_codec_window_boundary_noalloc_launch_v1": [_P] * 15 + [_U32, _U32],
     "statecentric_gdn_state_codec_boundary_scale_records_launch_v1": [_P] * 4 + [_U32],
     "statecentric_gdn_state_codec_window_boundary_cube_finish_launch_v1": [_P] * 16 + [_U32],
     "statecentric_gdn_state_codec_bf16_cube_matmul_launch_v1": [_P] * 4 + [_U32, _P, _P, _U32],

@@ -195,6 +195,27 @@ int32_t statecentric_gdn_state_codec_window_boundary_launch_v1(
     uint16_t* next_compensator_keys, uint16_t* next_compensator_values,
     float* residual_workspace, uint32_t states, uint32_t power_iterations);
 
+/* window_boundary_launch_v1 without the residual_workspace argument, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops and harnesses that forbid hipMalloc).  No counterpart exists in
+ * the reference.  The power refit's fitted residual goes to the library's own
+ * 32 MiB scratch array, one per GPU (held from the library's first use on that
+ * GPU until the process ends), so power_iterations in 1..32 admits
+ * 1 <= states <= 512; power_iterations == 0 needs no workspace and admits
+ * 1 <= states <= 16384.  Out-of-range counts and null pointers return 1, a
+ * failed lookup of the scratch array's device address returns 5.  The call
+ * allocates nothing.  Outputs are bit-identical to window_boundary_launch_v1.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time
+ * on one GPU (other streams, other host threads) race on it. */
+int32_t statecentric_gdn_state_codec_window_boundary_noalloc_launch_v1(
+    void* stream, const int8_t* residual, const float* smoothing,
+    const float* scales, const uint16_t* compensator_keys,
+    const uint16_t* compensator_values, float* record_decay,
+    uint16_t* record_keys, uint16_t* record_corrections, uint32_t* positions,
+    int8_t* next_residual, float* next_smoothing, float* next_scales,
+    uint16_t* next_compensator_keys, uint16_t* next_compensator_values,
+    uint32_t states, uint32_t power_iterations);
+
 /* scaled_record_keys[s][j][k] = fp16(key_j[k] * fp16(prod_{i>j} gate_i)), the
  * gate product taken in ascending order; 1 <= states <= 128.  Replaces
  * windowed_gdn_kernel.h:62-67 (window_boundary.cpp:537-587, 698-712). */

@@ -170,6 +170,22 @@ def test_boundary_entry_points_admit_like_the_reference(lib):
     assert lib.bf16_cube_matmul_launch_v1(None, p, p, p, 130, p, p, 65) == 1
 
 
+def test_noalloc_refit_admission(lib):
+    """The allocation-free refit: every pointer required, at most 512 states
+    when the power refit needs the scratch workspace, 16384 without it, and
+    at most 32 iterations; all rejected before any HIP call."""
+    p = ctypes.c_void_p(16)
+    fourteen = [p] * 14
+    assert lib.window_boundary_noalloc_launch_v1(None, *fourteen, 8, 33) == 1
+    for states, iterations in ((0, 0), (0, 4), (16385, 0), (513, 1), (513, 32), (4096, 4)):
+        assert lib.window_boundary_noalloc_launch_v1(None, *fourteen, states, iterations) == 1
+    for i in range(14):
+        args = list(fourteen)
+        args[i] = None
+        assert lib.window_boundary_noalloc_launch_v1(None, *args, 8, 0) == 1
+        assert lib.window_boundary_noalloc_launch_v1(None, *args, 8, 4) == 1
+
+
 def test_boundary_runtime_lifecycle(lib):
     """boundary_runtime.cpp:60-128."""
     p = ctypes.c_void_p(16)
