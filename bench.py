@@ -716,6 +716,8 @@ def bench_pool(steps: int, warmup: int, dtype_name: str):
     _log(f"config 5: generating a {dtype_name} pool {layers}x{slots}x{heads}x128x128")
     pool = torch.empty((layers, slots, heads, 128, 128), dtype=dtype, device=dev)
     for layer in range(layers):
+        if layer % 10 == 0:
+            _log(f"config 5: pool layers {layer}..{min(layer + 10, layers) - 1}")
         # Student-t(3) = Z / sqrt(chi2_3 / 3), chi2_3 a sum of three squared normals.
         for part in range(0, slots, 256):
             shape = (min(256, slots - part), heads, 128, 128)
