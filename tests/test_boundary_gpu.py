@@ -212,3 +212,23 @@ def test_quant_only_refit_outside_the_fast_division_domain(device):
     W.window_boundary_quant_only(ref, ref_out)
     assert_same(from_device(do, out), ref_out, OUT_NAMES)
     assert_same(from_device(d, buf), ref, buf.keys())
+
+
+def test_quant_only_refit_at_fp16_ties(device):
+    """The window whose requantization lands on fp16 ties (and within half an
+    fp16 ulp of them): the GPU's fp16 cast and round-to-even agree with the
+    oracle on every code."""
+    from test_boundary_oracle import tie_window
+
+    buf, _, _ = tie_window()
+    print("quant-only refit at fp16 ties, states=2", flush=True)
+    out = sentinel_outputs(2)
+    d, do = to_device(buf, device), to_device(out, device)
+    workspace = torch.zeros(16, dtype=torch.float32, device=device)
+    assert native().window_boundary_launch_v1(
+        stream(), *window_ptrs(d), *out_ptrs(do), workspace.data_ptr(), 2, 0) == 0
+    torch.cuda.synchronize()
+    ref, ref_out = WG.copy_buffers(buf), WG.copy_buffers(out)
+    W.window_boundary_quant_only(ref, ref_out)
+    assert_same(from_device(do, out), ref_out, OUT_NAMES)
+    assert_same(from_device(d, buf), ref, buf.keys())

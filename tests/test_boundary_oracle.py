@@ -177,3 +177,115 @@ def test_power_refit_fits_and_reencodes_the_window(iterations):
             assert sigma[0] > 2 * sigma[1]
             assert abs(nv[:, 0] @ vt[0]) > 0.999
             assert abs(np.linalg.norm(nk[:, 0]) - sigma[0]) < 1e-2 * sigma[0]
+
+
+def tie_window():
+    """Two full windows whose quant-only refit lands on fp16 ties.  Codes 0,
+    smoothing 1, every gate 1 (S = 1, suffixes 1) and a single non-zero record
+    (the last), so w[k][v] = key[k] * corr[v] exactly (an fp16 x fp16 product)
+    and m = w.
+
+    * State 0: key[0] = 127 and key[k] = k - 0.5, corr[v] = +-1, so
+      scale' = 127, the multiplier 127 / scale' is 1 and
+      t = m * (127 / scale') is exactly k - 0.5: every cell is a tie.
+    * State 1: key[0] = 126, corr[v] = +-(1 + v 2^-10), so the multiplier
+      127 / scale' rounds, and key[k] is the fp16 value nearest to
+      (k - 0.5) 126 / 127: t lands near the ties, often inside half an fp16
+      ulp of one without equalling it."""
+    buf = WG.window_buffers(2, 97, VK, positions=16)
+    buf["residual"][:] = 0
+    buf["smoothing"][:] = 1.0
+    buf["scales"][:] = 1.0
+    buf["record_decay"][:] = 1.0
+    keys = np.zeros((2, 16, 128), np.float32)
+    corr = np.zeros((2, 16, 128), np.float32)
+    k = np.arange(128, dtype=np.float32)
+    sign = np.where(np.arange(128) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    keys[0, 15] = k - 0.5
+    keys[0, 15, 0] = 127.0
+    corr[0, 15] = sign
+    keys[1, 15] = ((k - 0.5) * 126.0 / 127.0).astype(np.float16).astype(np.float32)
+    keys[1, 15, 0] = 126.0
+    corr[1, 15] = sign * (1.0 + np.arange(128, dtype=np.float32) * 2.0 ** -10)
+    buf["record_keys"] = keys.astype(np.float16).view(np.uint16)
+    buf["record_corrections"] = corr.astype(np.float16).view(np.uint16)
+    assert np.array_equal(W.f16_to_f32(buf["record_keys"]), keys)  # every value is fp16
+    assert np.array_equal(W.f16_to_f32(buf["record_corrections"]), corr)
+    return buf, keys[:, 15], corr[:, 15]
+
+
+def test_quant_only_refit_rounds_fp16_ties_to_even():
+    """window_boundary.cpp:465-475: t = m * (127 / scale'), clamped, cast to
+    fp16 (round to nearest even) and then to int8 with CAST_RINT (ties to
+    even).  At exact ties that is rint, not lround (half away from zero); near
+    ties the fp16 cast comes first, so a t just off a tie still rounds as the
+    tie.  The expectation is numpy's IEEE fp32 / fp16 arithmetic and rint."""
+    buf, keys, corr = tie_window()
+    out = W.boundary_outputs(2)
+    W.window_boundary_quant_only(buf, out)
+    codes = out["next_residual"].astype(np.int64)           # [state][v][k]
+    w = (corr[:, :, None] * keys[:, None, :]).astype(np.float32)   # exact products
+    scale = np.abs(w).max(axis=2)
+    assert np.array_equal(out["next_scales"], scale.astype(np.float32))
+    multiplier = (np.float32(127.0) / scale).astype(np.float32)
+    t = np.clip((w * multiplier[:, :, None]).astype(np.float32), -127, 127)
+    expected = np.rint(t.astype(np.float16).astype(np.float32)).astype(np.int64)
+    assert np.array_equal(codes, expected)
+    # State 0: every key but 0 is an exact tie k - 0.5; rint and lround differ
+    # on the 64 ties with an even integer part (0.5, 2.5, ..., 126.5) per column.
+    lround = (np.sign(t) * np.floor(np.abs(t) + 0.5)).astype(np.int64)
+    assert (codes[0] != lround[0]).sum() == 128 * 64
+    # State 1: cells where the fp16 cast decides (rint without it differs), and
+    # where lround differs.
+    without_cast = np.rint(t).astype(np.int64)
+    assert (codes[1] != without_cast[1]).sum() > 500
+    assert (codes[1] != lround[1]).sum() > 1000
+
+
+@pytest.mark.parametrize("iterations", [1, 4, 32])
+def test_power_refit_oracle_equals_a_numpy_transcription(iterations):
+    """The C oracle's power refit against a second transcription of the
+    reference kernel (tests/powerfit_numpy.py, numpy float32 in the reference's
+    statement order), every output bit: codes, smoothing, scales, fp16
+    compensators and the fitted residual.  With one iteration the result
+    depends on the start vector ((r+1)(c+3) mod 17 - 8, window_boundary.cpp:270)
+    and on the 20-step Newton square root (:17-23): a start vector off by one in
+    the column or a correctly rounded sqrt changes the bits, so each is pinned."""
+    import powerfit_numpy as P
+
+    states = 3
+    buf = planted_window(states, 101 + iterations)
+    out = W.boundary_outputs(states)
+    workspace = np.zeros((states, 128, 128), np.float32)
+    ref = WG.copy_buffers(buf)
+    W.window_boundary_power(ref, out, workspace, iterations)
+    for s in range(states):
+        got = P.power_refit(buf, s, iterations)
+        for name in ("next_residual", "next_smoothing", "next_scales", "next_compensator_keys",
+                     "next_compensator_values"):
+            assert got[name].tobytes() == out[name][s].tobytes(), (s, name)
+        assert got["workspace"].tobytes() == workspace[s].tobytes(), s
+    if iterations == 1:
+        shifted = P.power_refit(buf, 0, 1, start=lambda r: (
+            (((r + 1) * (np.arange(128) + 4)) % 17) - 8).astype(np.float32))
+        assert shifted["next_compensator_values"].tobytes() != \
+            out["next_compensator_values"][0].tobytes()
+        rounded = P.power_refit(buf, 0, 1, sqrt=lambda v: np.float32(np.sqrt(v)))
+        assert rounded["next_smoothing"].tobytes() != out["next_smoothing"][0].tobytes()
+
+
+def test_newton_square_root_transcription():
+    """The transcription's 20-step Newton root: exact on perfect squares and,
+    started at max(v, 1), still far from converged for large v (2^60 gives
+    about 2^40, not 2^30) -- the reference's own behaviour, which the oracle
+    shares (boundary_sqrt)."""
+    import powerfit_numpy as P
+
+    for n in (1, 2, 3, 7, 100, 4095):
+        assert P.square_root(np.float32(n * n)) == np.float32(n)
+    big = P.square_root(np.float32(2.0 ** 60))
+    assert 2.0 ** 39 < big < 2.0 ** 41
+    values = np.float32(10.0) ** np.linspace(-30, 30, 61).astype(np.float32)
+    want = np.array([P.square_root(v) for v in values], np.float32)
+    sqrt_c = W._bind_boundary(W._l()).gdn_oracle_boundary_sqrt
+    assert np.array_equal(np.array([sqrt_c(float(v)) for v in values], np.float32), want)
