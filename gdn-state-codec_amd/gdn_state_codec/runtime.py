@@ -1,25 +1,31 @@
-"""Slot runtime for the GDN state codec on MI355X.
+"""Compressed-slot runtime of the GDN state codec on MI355X.
 
-Mirrors the device-facing part of the reference's ``GdnStateCodecRuntime``
-(``src/gdn_state_codec/runtime.py``):
+The reference keeps, per GDN layer, a map from the vLLM cache index to an
+encoded slot and advances the slot one decode token at a time
+(``src/gdn_state_codec/runtime.py:275-868``).  This module offers the same
+service on the gfx950 library, assembled from this package's own parts:
 
-* the library loader keyed on the reference's library file names and symbols
-  (``_GdnStateCodecLibraries``, ``:48-274``), including the decode and boundary
-  runtime handles;
-* quant-only slot encoding of a provider state ``[H,V,K]``
-  (``_encode_quant_only_provider``, ``:460-547``) and the slot buffers
-  (``_allocate_slot``, ``:392-458``);
-* the per-token windowed decode ``step`` on the vector or cube backend
-  (``:750-843``) and the window-boundary refit every 16 tokens
-  (``_refit_boundary``, ``:627-741``);
-* the slot map keyed on the cache index, invalidation, fallback bookkeeping
-  and ``reconstruct`` (``:549-625``).
+* :class:`_GdnStateCodecLibraries` resolves every entry point through the
+  library file names the reference's ``ctypes`` loader opens
+  (``runtime.py:48-274``), so a library directory laid out for the reference
+  serves this runtime unchanged;
+* a :class:`_Slot` is a :class:`~gdn_state_codec.window.WindowSlot` (the live
+  boundary and its 16-record window) plus a spare boundary generation: a
+  window-boundary refit writes the spare and the two trade places, so the
+  refit never reads and writes the same buffers;
+* :class:`GdnStateCodecRuntime` owns the slots of one layer: it encodes a
+  provider state on the first decode of a cache index, validates every token's
+  tensors against a contract fixed by the slot's head count, folds a full
+  window into a new boundary before the next token, and runs the vector or
+  cube decode backend.
 
-Names, argument meaning and error behaviour follow the reference: contract
-violations and non-zero launch statuses raise ``RuntimeError``.  The vLLM
-configuration parsing, shadow observers and the exact-SVD initializer are not
-part of this build; :class:`GdnStateCodecExperiment` carries only the fields
-the runtime reads.
+The interface is the reference runtime's: the method names
+(``_encode_quant_only_provider``, ``reconstruct``, ``project``, ``_slot``,
+``invalidate``, ``decode_fallback_reason``, ``fall_back_to_native``, ``step``),
+the slot buffer names, the fallback reason keys, and ``RuntimeError`` for a
+violated contract or a non-zero launch status.  vLLM configuration parsing,
+the shadow observers and the exact-SVD initializer are not part of this
+build; :class:`GdnStateCodecExperiment` carries only the fields read here.
 """
 
 from __future__ import annotations
@@ -27,19 +33,22 @@ from __future__ import annotations
 import ctypes
 from dataclasses import dataclass, field
 from pathlib import Path
+from typing import Callable
 
 import torch
 
 from . import codec
 from ._native import OTHER_SIGNATURES, SIGNATURES, library_dir as default_library_dir
+from .window import POSITION_STRIDE, RANK, WINDOW, WindowSlot
 
-KEY_DIMENSION = 128
-VALUE_DIMENSION = 128
-COMPENSATOR_RANK = 4
-WINDOW_SIZE = 16
-POSITION_STRIDE = 8
-# Provider-launch admission of the reference (gdn_state_codec_quantize.cpp:207-211).
-PROVIDER_STATE_LIMIT = 64
+DIM = 128
+QWEN_QUERY_SCALE = DIM ** -0.5
+# The reference's provider launchers admit at most 64 states per call
+# (gdn_state_codec_quantize.cpp:207-211); larger slots use the batched encode.
+PROVIDER_LAUNCH_STATES = 64
+# The Cube-backed refit entry points admit at most 128 states
+# (window_boundary.cpp:698-703, 724-731).
+CUBE_REFIT_STATES = 128
 
 
 @dataclass
@@ -61,29 +70,6 @@ class GdnStateCodecExperiment:
             raise RuntimeError("gdn_state_codec.boundary_power_iterations must be in [0,32]")
         if self.decode_backend not in ("vector", "cube"):
             raise RuntimeError("gdn_state_codec.decode_backend must be 'vector' or 'cube'")
-
-
-@dataclass(slots=True)
-class _EncodedSlot:
-    residual: torch.Tensor
-    smoothing: torch.Tensor
-    scales: torch.Tensor
-    compensator_keys: torch.Tensor
-    compensator_values: torch.Tensor
-    record_decay: torch.Tensor
-    record_keys: torch.Tensor
-    record_corrections: torch.Tensor
-    positions: torch.Tensor
-    scratch_residual: torch.Tensor
-    scratch_smoothing: torch.Tensor
-    scratch_scales: torch.Tensor
-    scratch_compensator_keys: torch.Tensor
-    scratch_compensator_values: torch.Tensor
-    residual_workspace: torch.Tensor
-    scaled_record_keys: torch.Tensor
-    output: torch.Tensor
-    kernel_state_pointers: tuple[int, ...] = ()
-    steps: int = 0
 
 
 class _GdnStateCodecLibraries:
@@ -175,9 +161,130 @@ class _GdnStateCodecLibraries:
             self._boundary_handle = None
 
 
+# ------------------------------------------------------------------- slots
+
+_BOUNDARY_FIELDS = ("residual", "smoothing", "scales", "compensator_keys",
+                    "compensator_values")
+
+
+@dataclass
+class _Generation:
+    """One encoded boundary of H heads: int8 codes [H][value][key], fp32
+    smoothing [H][key] and scales [H][value], fp16 rank-4 compensators."""
+
+    residual: torch.Tensor
+    smoothing: torch.Tensor
+    scales: torch.Tensor
+    compensator_keys: torch.Tensor
+    compensator_values: torch.Tensor
+
+    def blank(self) -> "_Generation":
+        """Uninitialised buffers of the same geometry (a refit's destination)."""
+        return _Generation(*(torch.empty_like(getattr(self, name)) for name in _BOUNDARY_FIELDS))
+
+
+class _Slot:
+    """The compressed state of one cache index.
+
+    ``window`` holds the live boundary and its record window in the layout the
+    step and refit kernels read; ``spare`` is the boundary generation the next
+    refit writes.  ``residual_workspace`` serves the refit (the power
+    iteration's fitted residual, or the Cube record merge), ``scaled_record_keys``
+    the Cube record scaling, ``output`` the step's bf16 result.  ``steps``
+    counts the tokens recorded since the live boundary was formed."""
+
+    def __init__(self, boundary: _Generation) -> None:
+        heads = boundary.residual.shape[0]
+        device = boundary.residual.device
+        self.window = WindowSlot(
+            *(getattr(boundary, name) for name in _BOUNDARY_FIELDS),
+            record_decay=torch.ones((heads, WINDOW), dtype=torch.float32, device=device),
+            record_keys=torch.zeros((heads, WINDOW, DIM), dtype=torch.float16, device=device),
+            record_corrections=torch.zeros((heads, WINDOW, DIM), dtype=torch.float16,
+                                           device=device),
+            positions=torch.zeros((heads, POSITION_STRIDE), dtype=torch.int32, device=device))
+        self.spare = boundary.blank()
+        self.residual_workspace = torch.empty((heads, DIM, DIM), dtype=torch.float32,
+                                              device=device)
+        self.scaled_record_keys = torch.empty((heads, WINDOW, DIM), dtype=torch.float16,
+                                              device=device)
+        self.output = torch.empty((1, 1, heads, DIM), dtype=torch.bfloat16, device=device)
+        self.steps = 0
+
+    @property
+    def heads(self) -> int:
+        return self.window.states
+
+    @property
+    def window_full(self) -> bool:
+        return self.steps >= WINDOW
+
+    def trade_generations(self) -> None:
+        """Make the freshly written spare boundary live; the old one becomes the spare."""
+        for name in _BOUNDARY_FIELDS:
+            live, fresh = getattr(self.window, name), getattr(self.spare, name)
+            setattr(self.window, name, fresh)
+            setattr(self.spare, name, live)
+        self.steps = 0
+
+    def __getattr__(self, name: str):
+        # The slot buffer names of the reference runtime (runtime.py:25-45)
+        # read through to the live window.
+        window = self.__dict__.get("window")
+        if window is not None and name in WindowSlot.__dataclass_fields__:
+            return getattr(window, name)
+        raise AttributeError(name)
+
+
+# ---------------------------------------------------------- token contract
+
+@dataclass(frozen=True)
+class _Expect:
+    shape: tuple
+    dtype: torch.dtype
+
+
+def _token_contract(heads: int) -> dict[str, _Expect]:
+    """The tensors of one Qwen3.5 decode token for a slot of `heads` value
+    heads: query and key per GQA pair, value per head, gate inputs per head."""
+    pair = (1, 1, heads // 2, DIM)
+    return {"query": _Expect(pair, torch.bfloat16), "key": _Expect(pair, torch.bfloat16),
+            "value": _Expect((1, 1, heads, DIM), torch.bfloat16),
+            "log_decay": _Expect((1, 1, heads), torch.float32),
+            "beta": _Expect((1, 1, heads), torch.bfloat16)}
+
+
+def _enforce(tensor: torch.Tensor, what: str, expect: _Expect, device) -> None:
+    if (not isinstance(tensor, torch.Tensor) or tuple(tensor.shape) != expect.shape
+            or tensor.dtype != expect.dtype or not tensor.is_contiguous()
+            or tensor.device != device):
+        got = (f"{tensor.dtype} {tuple(tensor.shape)} on {tensor.device}, "
+               f"{'' if tensor.is_contiguous() else 'not '}contiguous"
+               if isinstance(tensor, torch.Tensor) else type(tensor).__name__)
+        raise RuntimeError(f"GDN State Codec: {what} must be a contiguous {expect.dtype} "
+                           f"tensor {expect.shape} on {device}; got {got}")
+
+
+def _launched(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"GDN State Codec {what} returned status {status}")
+
+
+# ------------------------------------------------------------------ runtime
+
+# Why a decode invocation must use the dense recurrent op, tested in order
+# (the reference's reason keys, runtime.py:567-585).
+_FALLBACK_RULES: tuple[tuple[str, Callable[..., bool]], ...] = (
+    ("speculative decode", lambda p, d, spec, n: spec),
+    ("mixed prefill/decode batch", lambda p, d, spec, n: p > 0 and d > 0),
+    ("multi-request decode batch",
+     lambda p, d, spec, n: d > 0 and (d != 1 or (n is not None and n != 1))),
+)
+
+
 class GdnStateCodecRuntime:
-    """Per-layer compressed-slot runtime: quant-only initializer, windowed
-    decode step, window-boundary refit."""
+    """The compressed slots of one GDN layer: quant-only initializer, windowed
+    decode step on the vector or cube backend, window-boundary refit."""
 
     def __init__(self, experiment: GdnStateCodecExperiment | None = None,
                  prefix: str = "", library_dir: Path | None = None) -> None:
@@ -187,8 +294,8 @@ class GdnStateCodecRuntime:
         self.experiment = experiment
         self.prefix = prefix
         self._libraries = _GdnStateCodecLibraries(experiment.library_dir)
-        self._slots: dict[int, _EncodedSlot] = {}
-        self._input_contract_validated = False
+        self._slots: dict[int, _Slot] = {}
+        self._contracts: dict[int, dict[str, _Expect]] = {}
         self.boundary_refits = 0
         self.native_fallbacks = 0
         self.native_fallback_reasons: dict[str, int] = {}
@@ -206,236 +313,171 @@ class GdnStateCodecRuntime:
     def _stream() -> int:
         return torch.cuda.current_stream().cuda_stream
 
-    @staticmethod
-    def _allocate_slot(residual, smoothing, scales, compensator_keys,
-                       compensator_values) -> _EncodedSlot:
-        heads = residual.shape[0]
-        device = residual.device
-        record_keys = torch.zeros((heads, WINDOW_SIZE, KEY_DIMENSION),
-                                  dtype=torch.float16, device=device)
-        slot = _EncodedSlot(
-            # [value,key]: one contiguous 128-byte int8 row per output value.
-            residual=residual,
-            smoothing=smoothing,
-            scales=scales,
-            compensator_keys=compensator_keys,
-            compensator_values=compensator_values,
-            record_decay=torch.ones((heads, WINDOW_SIZE), dtype=torch.float32, device=device),
-            record_keys=record_keys,
-            record_corrections=torch.zeros((heads, WINDOW_SIZE, VALUE_DIMENSION),
-                                           dtype=torch.float16, device=device),
-            # Read by the kernels as uint32 window positions.
-            positions=torch.zeros((heads, POSITION_STRIDE), dtype=torch.int32, device=device),
-            scratch_residual=torch.empty_like(residual),
-            scratch_smoothing=torch.empty_like(smoothing),
-            scratch_scales=torch.empty_like(scales),
-            scratch_compensator_keys=torch.empty_like(compensator_keys),
-            scratch_compensator_values=torch.empty_like(compensator_values),
-            residual_workspace=torch.empty(residual.shape, dtype=torch.float32, device=device),
-            scaled_record_keys=torch.empty_like(record_keys),
-            output=torch.empty((1, 1, heads, VALUE_DIMENSION), dtype=torch.bfloat16,
-                               device=device),
-        )
-        slot.kernel_state_pointers = GdnStateCodecRuntime._pointers(slot)
+    @property
+    def _cube_refit(self) -> bool:
+        """The quant-only refit folds the records with the Cube record GEMM, as
+        the reference runtime does when no power iterations are configured."""
+        return self.experiment.boundary_power_iterations == 0
+
+    # -- slot map ------------------------------------------------------------
+
+    def _slot(self, provider_state: torch.Tensor, cache_index: int) -> _Slot:
+        """The slot of `cache_index`, encoded from provider_state[cache_index]
+        on first use."""
+        slot = self._slots.get(cache_index)
+        if slot is None:
+            if not 0 <= cache_index < provider_state.shape[0]:
+                raise RuntimeError(f"GDN State Codec: cache index {cache_index} is out of range "
+                                   f"for a provider state of {provider_state.shape[0]} slots")
+            slot = self._encode_quant_only_provider(provider_state[cache_index])
+            if self._cube_refit:
+                self._libraries.boundary_handle(slot.heads)
+            self._slots[cache_index] = slot
         return slot
 
-    @staticmethod
-    def _pointers(slot: _EncodedSlot) -> tuple[int, ...]:
-        return (slot.residual.data_ptr(), slot.smoothing.data_ptr(), slot.scales.data_ptr(),
-                slot.compensator_keys.data_ptr(), slot.compensator_values.data_ptr(),
-                slot.record_decay.data_ptr(), slot.record_keys.data_ptr(),
-                slot.record_corrections.data_ptr(), slot.positions.data_ptr())
-
-    def _encode_quant_only_provider(self, provider_dense: torch.Tensor) -> _EncodedSlot:
-        if provider_dense.ndim != 3 or tuple(provider_dense.shape[-2:]) != (
-            VALUE_DIMENSION,
-            KEY_DIMENSION,
-        ):
-            raise RuntimeError("GDN State Codec requires provider states shaped [H,128,128]")
-        if provider_dense.dtype != torch.float32:
-            raise RuntimeError("GDN State Codec provider state must be FP32")
-        if not provider_dense.is_contiguous():
-            raise RuntimeError("GDN State Codec provider state must be contiguous")
-        if not provider_dense.is_cuda:
-            raise RuntimeError("GDN State Codec provider state must be a device tensor")
-        heads = provider_dense.shape[0]
-        device = provider_dense.device
-        residual = torch.empty_like(provider_dense, dtype=torch.int8)
-        smoothing = torch.empty((heads, KEY_DIMENSION), dtype=torch.float32, device=device)
-        scales = torch.empty((heads, VALUE_DIMENSION), dtype=torch.float32, device=device)
-        compensator_keys = torch.zeros((heads, KEY_DIMENSION, COMPENSATOR_RANK),
-                                       dtype=torch.float16, device=device)
-        compensator_values = torch.zeros((heads, VALUE_DIMENSION, COMPENSATOR_RANK),
-                                         dtype=torch.float16, device=device)
-        stream = self._stream()
-        if heads <= PROVIDER_STATE_LIMIT:
-            status = self._libraries.provider_initialize(
-                stream, provider_dense.data_ptr(), smoothing.data_ptr(),
-                residual.data_ptr(), scales.data_ptr(), heads)
-            what = "provider initializer"
-        else:
-            status = self._libraries.encode(
-                stream, provider_dense.data_ptr(), residual.data_ptr(),
-                smoothing.data_ptr(), scales.data_ptr(), heads, codec.LAYOUT_VALUE_KEY)
-            what = "batched provider encode"
-        if status != 0:
-            raise RuntimeError(f"GDN State Codec {what} launch failed: {status}")
-        return self._allocate_slot(residual, smoothing, scales, compensator_keys,
-                                   compensator_values)
-
-    def reconstruct(self, slot: _EncodedSlot) -> torch.Tensor:
-        """Dense [H,K,V] fp32 boundary of a quant-only slot, dequantized on the GPU.
-
-        Rounds as the portable C++ DequantizeBoundary (((s*code)/127)*scale),
-        which the reference's torch expression only approximates."""
-        dense = torch.empty(slot.residual.shape, dtype=torch.float32,
-                            device=slot.residual.device)
-        status = self._libraries.decode(
-            self._stream(), slot.residual.data_ptr(), slot.smoothing.data_ptr(),
-            slot.scales.data_ptr(), None, None, dense.data_ptr(), slot.residual.shape[0],
-            codec.LAYOUT_VALUE_KEY)
-        if status != 0:
-            raise RuntimeError(f"GDN State Codec decode launch failed: {status}")
-        return dense.transpose(-2, -1)
-
-    def project(self, slot: _EncodedSlot, query: torch.Tensor,
-                query_scale: float = KEY_DIMENSION ** -0.5) -> torch.Tensor:
-        """Boundary readout of a slot for one decode query [1,1,H/2,128] bf16.
-
-        Returns [1,1,H,128] fp32: sum_k code(v,k) s[k] (query_scale q[h/2,k]) / 127 * scale[v]."""
-        heads = slot.residual.shape[0]
-        if tuple(query.shape) != (1, 1, heads // 2, KEY_DIMENSION):
-            raise RuntimeError("GDN State Codec Qwen3.5 gate requires [1,1,H/2,128] query")
-        if query.dtype != torch.bfloat16 or not query.is_contiguous():
-            raise RuntimeError("GDN State Codec Qwen3.5 gate requires contiguous BF16 query")
-        out = torch.empty((1, 1, heads, VALUE_DIMENSION), dtype=torch.float32,
-                          device=slot.residual.device)
-        status = self._libraries.project_decode(
-            self._stream(), slot.residual.data_ptr(), slot.smoothing.data_ptr(),
-            slot.scales.data_ptr(), query.data_ptr(), out.data_ptr(), 1, heads,
-            heads // 2, float(query_scale), codec.LAYOUT_VALUE_KEY)
-        if status != 0:
-            raise RuntimeError(f"GDN State Codec projection launch failed: {status}")
-        return out
-
-    def invalidate(self, cache_indices: tuple[int, ...]) -> None:
+    def invalidate(self, cache_indices) -> None:
+        """Forget the slots of `cache_indices` (their dense state changed)."""
         for cache_index in cache_indices:
             self._slots.pop(cache_index, None)
 
     @staticmethod
     def decode_fallback_reason(*, num_prefills: int, num_decodes: int, speculative: bool,
                                cache_index_count: int | None = None) -> str | None:
-        """Return why an invocation must use the dense recurrent op (runtime.py:567-585)."""
-        if speculative:
-            return "speculative decode"
-        if num_prefills > 0 and num_decodes > 0:
-            return "mixed prefill/decode batch"
-        if num_decodes > 0 and (
-            num_decodes != 1 or (cache_index_count is not None and cache_index_count != 1)
-        ):
-            return "multi-request decode batch"
+        """The reason key when this invocation must use the dense op, else None."""
+        for reason, applies in _FALLBACK_RULES:
+            if applies(num_prefills, num_decodes, speculative, cache_index_count):
+                return reason
         return None
 
     def fall_back_to_native(self, reason: str) -> None:
-        """Discard compressed slots before the provider updates dense state."""
+        """Drop every slot before the dense op updates the provider state, and count why."""
         self._slots.clear()
         self.native_fallbacks += 1
         self.native_fallback_reasons[reason] = self.native_fallback_reasons.get(reason, 0) + 1
 
-    def _use_cube_boundary(self) -> bool:
-        return self.experiment.boundary_power_iterations == 0
+    # -- boundary ------------------------------------------------------------
 
-    def _slot(self, provider_state: torch.Tensor, cache_index: int) -> _EncodedSlot:
-        slot = self._slots.get(cache_index)
-        if slot is not None:
-            return slot
-        if cache_index < 0 or cache_index >= provider_state.shape[0]:
-            raise RuntimeError("GDN State Codec cache index is out of range")
-        slot = self._encode_quant_only_provider(provider_state[cache_index])
-        if self._use_cube_boundary():
-            self._libraries.boundary_handle(slot.residual.shape[0])
-        self._slots[cache_index] = slot
-        return slot
-
-    def _refit_boundary(self, slot: _EncodedSlot) -> None:
-        """Fold a full window into a new boundary (runtime.py:627-741): the cube
-        record merge plus quant-only refit, or the power-iteration refit."""
-        stream = self._stream()
-        heads = slot.residual.shape[0]
-        use_cube = self._use_cube_boundary()
-        if use_cube:
-            handle = self._libraries.boundary_handle(heads)
-            status = self._libraries.boundary_runtime_step(
-                handle, stream, slot.record_decay.data_ptr(), slot.record_keys.data_ptr(),
-                slot.record_corrections.data_ptr(), slot.scaled_record_keys.data_ptr(),
-                slot.residual_workspace.data_ptr(), heads)
-            if status != 0:
-                raise RuntimeError(f"GDN State Codec Cube boundary merge failed: {status}")
-        pointers = (stream, *self._pointers(slot), slot.scratch_residual.data_ptr(),
-                    slot.scratch_smoothing.data_ptr(), slot.scratch_scales.data_ptr(),
-                    slot.scratch_compensator_keys.data_ptr(),
-                    slot.scratch_compensator_values.data_ptr(),
-                    slot.residual_workspace.data_ptr())
-        if use_cube:
-            status = self._libraries.window_boundary_cube_finish(*pointers, heads)
+    def _encode_quant_only_provider(self, provider_dense: torch.Tensor) -> _Slot:
+        """A new slot from one provider state [H][value][key] fp32 (device,
+        contiguous): codes, smoothing and scales of the quant-only initializer,
+        zero compensators, an empty window."""
+        if provider_dense.ndim != 3:
+            raise RuntimeError("GDN State Codec: the provider state must be [H,128,128] "
+                               f"(value x key per head), got {tuple(provider_dense.shape)}")
+        _enforce(provider_dense, "the provider state",
+                 _Expect((provider_dense.shape[0], DIM, DIM), torch.float32),
+                 provider_dense.device)
+        if not provider_dense.is_cuda:
+            raise RuntimeError("GDN State Codec: the provider state must live on the GPU")
+        heads, device = provider_dense.shape[0], provider_dense.device
+        boundary = _Generation(
+            residual=torch.empty((heads, DIM, DIM), dtype=torch.int8, device=device),
+            smoothing=torch.empty((heads, DIM), dtype=torch.float32, device=device),
+            scales=torch.empty((heads, DIM), dtype=torch.float32, device=device),
+            compensator_keys=torch.zeros((heads, DIM, RANK), dtype=torch.float16, device=device),
+            compensator_values=torch.zeros((heads, DIM, RANK), dtype=torch.float16,
+                                           device=device))
+        source = provider_dense.data_ptr()
+        codes, smoothing, scales = (boundary.residual.data_ptr(), boundary.smoothing.data_ptr(),
+                                    boundary.scales.data_ptr())
+        if heads <= PROVIDER_LAUNCH_STATES:  # the reference's own v3 entry point
+            _launched(self._libraries.provider_initialize(self._stream(), source, smoothing,
+                                                          codes, scales, heads),
+                      "provider initialize")
         else:
-            status = self._libraries.window_boundary(
-                *pointers, heads, self.experiment.boundary_power_iterations)
-        if status != 0:
-            raise RuntimeError(f"GDN State Codec boundary-refit launch failed: {status}")
-        slot.residual, slot.scratch_residual = slot.scratch_residual, slot.residual
-        slot.smoothing, slot.scratch_smoothing = slot.scratch_smoothing, slot.smoothing
-        slot.scales, slot.scratch_scales = slot.scratch_scales, slot.scales
-        slot.compensator_keys, slot.scratch_compensator_keys = (
-            slot.scratch_compensator_keys, slot.compensator_keys)
-        slot.compensator_values, slot.scratch_compensator_values = (
-            slot.scratch_compensator_values, slot.compensator_values)
-        slot.kernel_state_pointers = self._pointers(slot)
-        slot.steps = 0
+            _launched(self._libraries.encode(self._stream(), source, codes, smoothing, scales,
+                                             heads, codec.LAYOUT_VALUE_KEY), "batched encode")
+        return _Slot(boundary)
+
+    def reconstruct(self, slot: _Slot) -> torch.Tensor:
+        """The dense [H][key][value] fp32 boundary of a quant-only slot,
+        dequantized on the GPU in the portable reference's rounding order
+        ((s * code) / 127) * scale."""
+        dense = torch.empty((slot.heads, DIM, DIM), dtype=torch.float32,
+                            device=slot.window.device)
+        _launched(self._libraries.decode(
+            self._stream(), slot.residual.data_ptr(), slot.smoothing.data_ptr(),
+            slot.scales.data_ptr(), None, None, dense.data_ptr(), slot.heads,
+            codec.LAYOUT_VALUE_KEY), "decode")
+        return dense.transpose(-2, -1)
+
+    def project(self, slot: _Slot, query: torch.Tensor,
+                query_scale: float = QWEN_QUERY_SCALE) -> torch.Tensor:
+        """The boundary readout of a slot for one decode query, [1,1,H/2,128]
+        bf16 (value head h reads query head h/2); returns [1,1,H,128] fp32."""
+        _enforce(query, "the query", _Expect((1, 1, slot.heads // 2, DIM), torch.bfloat16),
+                 slot.window.device)
+        out = torch.empty((1, 1, slot.heads, DIM), dtype=torch.float32,
+                          device=slot.window.device)
+        _launched(self._libraries.project_decode(
+            self._stream(), slot.residual.data_ptr(), slot.smoothing.data_ptr(),
+            slot.scales.data_ptr(), query.data_ptr(), out.data_ptr(), 1, slot.heads,
+            slot.heads // 2, float(query_scale), codec.LAYOUT_VALUE_KEY), "projection")
+        return out
+
+    def _refit_boundary(self, slot: _Slot) -> None:
+        """Fold the slot's full window into a new boundary in its spare
+        generation, then make that generation live.  With no power iterations
+        the records are merged by the Cube record GEMM and requantized with the
+        existing smoothing; otherwise the rank-4 power iteration refits."""
+        stream, heads = self._stream(), slot.heads
+        destination = (slot.spare.residual.data_ptr(), slot.spare.smoothing.data_ptr(),
+                       slot.spare.scales.data_ptr(), slot.spare.compensator_keys.data_ptr(),
+                       slot.spare.compensator_values.data_ptr())
+        if self._cube_refit:
+            if heads > CUBE_REFIT_STATES:
+                raise RuntimeError(f"GDN State Codec: the Cube refit serves at most "
+                                   f"{CUBE_REFIT_STATES} heads, this slot has {heads}")
+            merge = slot.residual_workspace
+            _launched(self._libraries.boundary_runtime_step(
+                self._libraries.boundary_handle(heads), stream, slot.record_decay.data_ptr(),
+                slot.record_keys.data_ptr(), slot.record_corrections.data_ptr(),
+                slot.scaled_record_keys.data_ptr(), merge.data_ptr(), heads),
+                "Cube record merge")
+            _launched(self._libraries.window_boundary_cube_finish(
+                stream, *slot.window.pointers(), *destination, merge.data_ptr(), heads),
+                "Cube refit")
+        else:
+            _launched(self._libraries.window_boundary(
+                stream, *slot.window.pointers(), *destination,
+                slot.residual_workspace.data_ptr(), heads,
+                self.experiment.boundary_power_iterations), "power refit")
+        slot.trade_generations()
         self.boundary_refits += 1
+
+    # -- decode --------------------------------------------------------------
 
     def step(self, provider_state: torch.Tensor, cache_index: int, query: torch.Tensor,
              key: torch.Tensor, value: torch.Tensor, log_decay: torch.Tensor,
              beta: torch.Tensor, query_scale: float) -> torch.Tensor:
-        """One decode token of one request (runtime.py:750-843): refit a full
-        window first, then the windowed step; returns bf16 [1,1,H,128]."""
+        """One decode token of one request: the slot of `cache_index` (encoded
+        on first use) refits its boundary if its window is full, then takes the
+        windowed step.  Returns the bf16 output [1,1,H,128] (the slot's buffer)."""
         slot = self._slot(provider_state, cache_index)
-        if slot.steps == WINDOW_SIZE:
+        if slot.steps > WINDOW:
+            raise RuntimeError("GDN State Codec: slot window holds more than 16 records")
+        if slot.window_full:
             self._refit_boundary(slot)
-        elif slot.steps > WINDOW_SIZE:
-            raise RuntimeError("GDN State Codec runtime window position exceeded p=16")
-        heads = slot.residual.shape[0]
-        if not self._input_contract_validated:
-            query_shape = (1, 1, heads // 2, KEY_DIMENSION)
-            if tuple(query.shape) != query_shape or tuple(key.shape) != query_shape:
-                raise RuntimeError("GDN State Codec Qwen3.5 gate requires [1,1,H/2,128] query/key")
-            if tuple(value.shape) != (1, 1, heads, VALUE_DIMENSION):
-                raise RuntimeError("GDN State Codec Qwen3.5 gate requires [1,1,H,128] value")
-            if tuple(log_decay.shape) != (1, 1, heads) or tuple(beta.shape) != (1, 1, heads):
-                raise RuntimeError("GDN State Codec Qwen3.5 gate requires [1,1,H] decay/beta")
-            if log_decay.dtype != torch.float32:
-                raise RuntimeError("GDN State Codec Qwen3.5 gate requires FP32 log decay")
-            if query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16:
-                raise RuntimeError("GDN State Codec Qwen3.5 gate requires BF16 query/key")
-            if value.dtype != torch.bfloat16 or beta.dtype != torch.bfloat16:
-                raise RuntimeError("GDN State Codec Qwen3.5 gate requires BF16 value/beta")
-            if abs(query_scale - KEY_DIMENSION ** -0.5) > 1.0e-8:
-                raise RuntimeError("GDN State Codec Qwen3.5 query scale is unsupported")
-            if not all(t.is_contiguous() for t in (query, key, value, log_decay, beta)):
-                raise RuntimeError("GDN State Codec Qwen3.5 inputs must be contiguous")
-            self._input_contract_validated = True
-        pointers = (self._stream(), *slot.kernel_state_pointers, log_decay.data_ptr(),
-                    beta.data_ptr(), key.data_ptr(), query.data_ptr(), value.data_ptr(),
-                    slot.output.data_ptr())
-        if self.experiment.decode_backend == "vector":
-            vector_step = (self._libraries.window_step_bf16_quant_only
-                           if self.experiment.boundary_power_iterations == 0
-                           else self._libraries.window_step_bf16)
-            status = vector_step(*pointers, heads)
+        contract = self._contracts.get(slot.heads)
+        if contract is None:
+            contract = self._contracts.setdefault(slot.heads, _token_contract(slot.heads))
+        device = slot.window.device
+        for what, tensor in (("query", query), ("key", key), ("value", value),
+                             ("log_decay", log_decay), ("beta", beta)):
+            _enforce(tensor, what, contract[what], device)
+        if abs(query_scale - QWEN_QUERY_SCALE) > 1.0e-8:
+            raise RuntimeError(f"GDN State Codec: the decode kernels apply Qwen3.5's query "
+                               f"scale 128^-1/2, not {query_scale}")
+        operands = (*slot.window.pointers(), log_decay.data_ptr(), beta.data_ptr(),
+                    key.data_ptr(), query.data_ptr(), value.data_ptr(), slot.output.data_ptr(),
+                    slot.heads)
+        if self.experiment.decode_backend == "cube":
+            status = self._libraries.decode_runtime_step(
+                self._libraries.decode_handle(slot.heads), self._stream(), *operands)
+        elif self.experiment.boundary_power_iterations == 0:
+            status = self._libraries.window_step_bf16_quant_only(self._stream(), *operands)
         else:
-            handle = self._libraries.decode_handle(heads)
-            status = self._libraries.decode_runtime_step(handle, *pointers, heads)
-        if status != 0:
-            raise RuntimeError(f"GDN State Codec decode-step launch failed: {status}")
+            status = self._libraries.window_step_bf16(self._stream(), *operands)
+        _launched(status, f"{self.experiment.decode_backend} decode step")
         slot.steps += 1
         return slot.output

@@ -48,15 +48,52 @@ def test_runtime_contract_errors(device):
     state = torch.zeros((2, 4, 128, 128), dtype=torch.float32, device=device)
     with pytest.raises(RuntimeError, match="out of range"):
         runtime._slot(state, 2)
-    with pytest.raises(RuntimeError, match="FP32"):
+    with pytest.raises(RuntimeError, match="float32"):
         runtime._encode_quant_only_provider(state[0].to(torch.float16))
-    with pytest.raises(RuntimeError, match="contiguous"):
+    with pytest.raises(RuntimeError, match="not contiguous"):
         runtime._encode_quant_only_provider(state[0].transpose(-2, -1))
+    with pytest.raises(RuntimeError, match=r"\[H,128,128\]"):
+        runtime._encode_quant_only_provider(state)
     slot = runtime._slot(state, 0)
-    with pytest.raises(RuntimeError, match="H/2"):
+    with pytest.raises(RuntimeError, match=r"\(1, 1, 2, 128\)"):
         runtime.project(slot, torch.zeros((1, 1, 4, 128), dtype=torch.bfloat16, device=device))
     runtime.fall_back_to_native("multi-request decode batch")
     assert runtime.native_fallbacks == 1 and not runtime._slots
+    assert runtime.native_fallback_reasons == {"multi-request decode batch": 1}
+    runtime.close()
+
+
+def test_runtime_checks_every_token(device):
+    """The token contract is enforced on every call, not only the first: a
+    later token with a wrong shape, dtype, layout, device or query scale raises
+    before any launch and leaves the slot's window position unchanged."""
+    runtime = GdnStateCodecRuntime()
+    heads = 4
+    state = torch.zeros((1, heads, 128, 128), dtype=torch.float32, device=device)
+    bf = lambda *shape: torch.zeros(shape, dtype=torch.bfloat16, device=device)  # noqa: E731
+    good = dict(query=bf(1, 1, 2, 128), key=bf(1, 1, 2, 128), value=bf(1, 1, heads, 128),
+                log_decay=torch.zeros((1, 1, heads), dtype=torch.float32, device=device),
+                beta=bf(1, 1, heads))
+    run = lambda **kw: runtime.step(state, 0, query_scale=kw.pop("scale", 128 ** -0.5),  # noqa
+                                    **{**good, **kw})
+    run()
+    torch.cuda.synchronize()
+    slot = runtime._slot(state, 0)
+    assert slot.steps == 1
+    bad = {"query": bf(1, 1, 4, 128),
+           "key": bf(1, 1, 2, 256)[..., ::2],
+           "value": torch.zeros((1, 1, heads, 128), dtype=torch.float32, device=device),
+           "log_decay": torch.zeros((1, 1, heads), dtype=torch.float32),
+           "beta": bf(1, 1, heads + 2)}
+    for name, tensor in bad.items():
+        with pytest.raises(RuntimeError, match=name):
+            run(**{name: tensor})
+    with pytest.raises(RuntimeError, match="query scale"):
+        run(scale=1.0)
+    assert slot.steps == 1
+    run()
+    torch.cuda.synchronize()
+    assert slot.steps == 2 and int(slot.positions[0, 0]) == 2
     runtime.close()
 
 
