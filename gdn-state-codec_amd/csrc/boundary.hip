@@ -375,7 +375,11 @@ extern "C" int32_t statecentric_gdn_state_codec_window_boundary_launch_v1(
       !record_decay || !record_keys || !record_corrections || !positions || !next_residual ||
       !next_smoothing || !next_scales || !next_compensator_keys || !next_compensator_values ||
       !residual_workspace || states == 0 || states > gdn::kMaxWindowStates ||
-      power_iterations > 32) {
+      power_iterations > 32 ||
+      !gdn::aligned16(residual, smoothing, scales, compensator_keys, compensator_values,
+                      record_decay, record_keys, record_corrections, positions, next_residual,
+                      next_smoothing, next_scales, next_compensator_keys,
+                      next_compensator_values, residual_workspace)) {
     return gdn::kStatusInvalidArgument;
   }
   if (power_iterations > 0) {
@@ -401,7 +405,11 @@ extern "C" int32_t statecentric_gdn_state_codec_window_boundary_cube_finish_laun
   if (!residual || !smoothing || !scales || !compensator_keys || !compensator_values ||
       !record_decay || !record_keys || !record_corrections || !positions || !next_residual ||
       !next_smoothing || !next_scales || !next_compensator_keys || !next_compensator_values ||
-      !record_merge || states == 0 || states > gdn::kMaxCubeStates) {
+      !record_merge || states == 0 || states > gdn::kMaxCubeStates ||
+      !gdn::aligned16(residual, smoothing, scales, compensator_keys, compensator_values,
+                      record_decay, record_keys, record_corrections, positions, next_residual,
+                      next_smoothing, next_scales, next_compensator_keys,
+                      next_compensator_values, record_merge)) {
     return gdn::kStatusInvalidArgument;
   }
   const gdn::RefitArgs args{residual, smoothing, scales, record_decay, record_keys,
@@ -415,7 +423,8 @@ extern "C" int32_t statecentric_gdn_state_codec_boundary_scale_records_launch_v1
     void* stream, const float* record_decay, const uint16_t* record_keys,
     uint16_t* scaled_record_keys, uint32_t states) {
   if (!record_decay || !record_keys || !scaled_record_keys || states == 0 ||
-      states > gdn::kMaxCubeStates) {
+      states > gdn::kMaxCubeStates ||
+      !gdn::aligned16(record_decay, record_keys, scaled_record_keys)) {
     return gdn::kStatusInvalidArgument;
   }
   return gdn::launch_scale_records(stream, record_decay, record_keys, scaled_record_keys, states);
@@ -425,7 +434,8 @@ extern "C" int32_t statecentric_gdn_state_codec_bf16_cube_matmul_launch_v1(
     void* stream, const uint16_t* a, const uint16_t* b, float* c, uint32_t states,
     void* workspace, void* tiling, uint32_t blocks) {
   if (!a || !b || !c || !workspace || !tiling || blocks == 0 || blocks > 64 || states == 0 ||
-      states > gdn::kMaxCubeStates || blocks != (states + 1u) / 2u) {
+      states > gdn::kMaxCubeStates || blocks != (states + 1u) / 2u ||
+      !gdn::aligned16(a, b, c)) {
     return gdn::kStatusInvalidArgument;
   }
   return gdn::launch_f16_at_b(stream, a, b, c, states);
@@ -479,7 +489,9 @@ extern "C" int32_t statecentric_gdn_state_codec_boundary_runtime_step_v1(
     auto* runtime = static_cast<BoundaryRuntime*>(opaque);
     if (runtime == nullptr || runtime != boundary_runtime || !record_decay || !record_keys ||
         !record_corrections || !scaled_record_keys || !record_merge ||
-        states != runtime->states) {
+        states != runtime->states ||
+        !gdn::aligned16(record_decay, record_keys, record_corrections, scaled_record_keys,
+                        record_merge)) {
       return 1;
     }
   }

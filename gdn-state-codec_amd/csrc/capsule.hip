@@ -880,6 +880,9 @@ extern "C" int32_t statecentric_gdn_state_codec_capsule_serialize_launch_v1(
       !record_decay || !record_keys || !record_corrections || !positions || !capsules ||
       !offsets || !lengths || states == 0 || states > gdn::kMaxWindowStates ||
       (layout != gdn::kKeyValue && layout != gdn::kValueKey) ||
+      !gdn::aligned16(residual, smoothing, scales, compensator_keys, compensator_values,
+                      record_decay, record_keys, record_corrections, positions, capsules,
+                      offsets, lengths) ||
       !gdn::make_identity(geometry_sha256, generation, epoch, &args.identity)) {
     return gdn::kStatusInvalidArgument;
   }
@@ -919,6 +922,9 @@ extern "C" int32_t statecentric_gdn_state_codec_capsule_restore_launch_v1(
       !record_corrections || !positions || !status || states == 0 ||
       states > gdn::kMaxWindowStates ||
       (layout != gdn::kKeyValue && layout != gdn::kValueKey) ||
+      !gdn::aligned16(capsules, offsets, lengths, expected_positions, residual, smoothing,
+                      scales, compensator_keys, compensator_values, record_decay, record_keys,
+                      record_corrections, positions, status) ||
       !gdn::make_identity(geometry_sha256, generation, epoch, &args.identity)) {
     return gdn::kStatusInvalidArgument;
   }

@@ -581,7 +581,9 @@ using gdn::kStatusInvalidArgument;
 
 extern "C" int32_t statecentric_gdn_state_codec_smoothing_launch_v1(
     void* stream, const float* residual, float* smoothing) {
-  if (residual == nullptr || smoothing == nullptr) return kStatusInvalidArgument;
+  if (residual == nullptr || smoothing == nullptr || !gdn::aligned16(residual, smoothing)) {
+    return kStatusInvalidArgument;
+  }
   return gdn::launch_encode<gdn::kModeSmoothingOnly>(
       stream, residual, gdn::kDtypeF32, nullptr, smoothing, nullptr, nullptr, 1,
       gdn::kKeyValue, gdn::kIdentityMap);
@@ -591,7 +593,7 @@ extern "C" int32_t statecentric_gdn_state_codec_quantize_launch_v1(
     void* stream, const float* residual, const float* smoothing,
     int8_t* quantized, float* value_scales) {
   if (residual == nullptr || smoothing == nullptr || quantized == nullptr ||
-      value_scales == nullptr) {
+      value_scales == nullptr || !gdn::aligned16(residual, smoothing, quantized, value_scales)) {
     return kStatusInvalidArgument;
   }
   return gdn::launch_encode<gdn::kModeGivenSmoothing>(
@@ -605,7 +607,9 @@ extern "C" int32_t statecentric_gdn_state_codec_dequantize_launch_v1(
     const float* compensator_values, float* dense) {
   if (quantized == nullptr || smoothing == nullptr || value_scales == nullptr ||
       compensator_keys == nullptr || compensator_values == nullptr ||
-      dense == nullptr) {
+      dense == nullptr ||
+      !gdn::aligned16(quantized, smoothing, value_scales, compensator_keys,
+                      compensator_values, dense)) {
     return kStatusInvalidArgument;
   }
   return gdn::launch_decode<true>(stream, quantized, smoothing, value_scales,
@@ -618,7 +622,7 @@ extern "C" int32_t statecentric_gdn_state_codec_provider_smoothing_launch_v2(
     void* stream, const float* provider_state, float* smoothing,
     uint32_t states) {
   if (provider_state == nullptr || smoothing == nullptr ||
-      !gdn::provider_states_ok(states)) {
+      !gdn::provider_states_ok(states) || !gdn::aligned16(provider_state, smoothing)) {
     return kStatusInvalidArgument;
   }
   return gdn::launch_encode<gdn::kModeSmoothingOnly>(
@@ -631,7 +635,8 @@ extern "C" int32_t statecentric_gdn_state_codec_provider_quantize_launch_v2(
     int8_t* quantized, float* value_scales, uint32_t states) {
   if (provider_state == nullptr || smoothing == nullptr ||
       quantized == nullptr || value_scales == nullptr ||
-      !gdn::provider_states_ok(states)) {
+      !gdn::provider_states_ok(states) ||
+      !gdn::aligned16(provider_state, smoothing, quantized, value_scales)) {
     return kStatusInvalidArgument;
   }
   return gdn::launch_encode<gdn::kModeGivenSmoothing>(
@@ -646,7 +651,8 @@ extern "C" int32_t statecentric_gdn_state_codec_encode_launch_v4(
     float* value_scales, uint64_t heads, uint32_t layout) {
   if (state == nullptr || quantized == nullptr || smoothing == nullptr ||
       value_scales == nullptr || heads == 0 || heads > gdn::kMaxGrid ||
-      !gdn::valid_layout(layout)) {
+      !gdn::valid_layout(layout) ||
+      !gdn::aligned16(state, quantized, smoothing, value_scales)) {
     return kStatusInvalidArgument;
   }
   return gdn::launch_encode<gdn::kModeEncode>(
@@ -662,7 +668,9 @@ extern "C" int32_t statecentric_gdn_state_codec_decode_launch_v4(
   if (quantized == nullptr || smoothing == nullptr || value_scales == nullptr ||
       state == nullptr || heads == 0 || heads > gdn::kMaxGrid ||
       !gdn::valid_layout(layout) ||
-      (compensator_keys == nullptr) != (compensator_values == nullptr)) {
+      (compensator_keys == nullptr) != (compensator_values == nullptr) ||
+      !gdn::aligned16(quantized, smoothing, value_scales, compensator_keys,
+                      compensator_values, state)) {
     return kStatusInvalidArgument;
   }
   if (compensator_keys != nullptr) {
@@ -697,7 +705,8 @@ extern "C" int32_t statecentric_gdn_state_codec_pool_encode_launch_v4(
     float* value_scales) {
   if (pool == nullptr || quantized == nullptr || smoothing == nullptr ||
       value_scales == nullptr ||
-      !pool_args_ok(slot_ids, batch, layers, slots, heads, layout, pool_dtype)) {
+      !pool_args_ok(slot_ids, batch, layers, slots, heads, layout, pool_dtype) ||
+      !gdn::aligned16(pool, slot_ids, quantized, smoothing, value_scales)) {
     return kStatusInvalidArgument;
   }
   const gdn::TileMap map{slot_ids, batch, heads, slots};
@@ -713,7 +722,8 @@ extern "C" int32_t statecentric_gdn_state_codec_pool_decode_launch_v4(
     void* pool, uint32_t pool_dtype) {
   if (pool == nullptr || quantized == nullptr || smoothing == nullptr ||
       value_scales == nullptr ||
-      !pool_args_ok(slot_ids, batch, layers, slots, heads, layout, pool_dtype)) {
+      !pool_args_ok(slot_ids, batch, layers, slots, heads, layout, pool_dtype) ||
+      !gdn::aligned16(pool, slot_ids, quantized, smoothing, value_scales)) {
     return kStatusInvalidArgument;
   }
   const gdn::TileMap map{slot_ids, batch, heads, slots};

@@ -693,7 +693,8 @@ extern "C" int32_t statecentric_gdn_state_codec_prepare_int8_vector_launch_v1(
     void* stream, const uint16_t* input, const float* axis_scale, int8_t* quantized,
     float* dynamic_scale, uint32_t states) {
   if (!input || !axis_scale || !quantized || !dynamic_scale || states == 0 ||
-      states > gdn::kMaxWindowStates) {
+      states > gdn::kMaxWindowStates ||
+      !gdn::aligned16(input, axis_scale, quantized, dynamic_scale)) {
     return gdn::kStatusInvalidArgument;
   }
   return gdn::launch(gdn::prepare_vector_kernel, dim3((states + gdn::kWaves - 1) / gdn::kWaves),
@@ -705,7 +706,8 @@ extern "C" int32_t statecentric_gdn_state_codec_prepare_decode_pair_launch_v1(
     void* stream, const uint16_t* reads, const uint16_t* queries, const float* decay,
     const float* smoothing, int8_t* quantized, float* dynamic_scale, uint32_t states) {
   if (!reads || !queries || !decay || !smoothing || !quantized || !dynamic_scale ||
-      states == 0 || states > gdn::kMaxWindowStates) {
+      states == 0 || states > gdn::kMaxWindowStates ||
+      !gdn::aligned16(reads, queries, decay, smoothing, quantized, dynamic_scale)) {
     return gdn::kStatusInvalidArgument;
   }
   const gdn::VectorArgs in{nullptr, reads, queries, decay, nullptr, states, false};
@@ -716,7 +718,8 @@ extern "C" int32_t statecentric_gdn_state_codec_prepare_decode_pair_bf16_launch_
     void* stream, const uint16_t* keys, const uint16_t* queries, const float* decay,
     const float* smoothing, int8_t* quantized, float* dynamic_scale, uint32_t states) {
   if (!keys || !queries || !decay || !smoothing || !quantized || !dynamic_scale ||
-      states == 0 || states > gdn::kMaxWindowStates || states % 2 != 0) {
+      states == 0 || states > gdn::kMaxWindowStates || states % 2 != 0 ||
+      !gdn::aligned16(keys, queries, decay, smoothing, quantized, dynamic_scale)) {
     return gdn::kStatusInvalidArgument;
   }
   const gdn::VectorArgs in{keys, nullptr, queries, decay, nullptr, states, true};
@@ -727,7 +730,8 @@ extern "C" int32_t statecentric_gdn_state_codec_int8_cube_matmul_launch_v1(
     void* stream, const int8_t* a, const int8_t* b, int32_t* c, uint32_t states,
     uint32_t transpose_a, void* workspace, void* tiling, uint32_t blocks) {
   if (!a || !b || !c || !workspace || !tiling || blocks == 0 || blocks > 64 ||
-      states == 0 || states > 128 || blocks != (states + 1u) / 2u || transpose_a > 1u) {
+      states == 0 || states > 128 || blocks != (states + 1u) / 2u || transpose_a > 1u ||
+      !gdn::aligned16(a, b, c)) {
     return gdn::kStatusInvalidArgument;
   }
   return gdn::launch(gdn::int8_matmul_kernel, dim3(states), dim3(gdn::kThreads), stream,
@@ -744,7 +748,10 @@ extern "C" int32_t statecentric_gdn_state_codec_finish_decode_pair_launch_v1(
   if (!projected || !dynamic_scale || !scales || !compensator_keys || !compensator_values ||
       !record_decay || !record_keys || !record_corrections || !positions || !decay ||
       !write_keys || !reads || !queries || !values || !outputs || states == 0 ||
-      states > gdn::kMaxWindowStates) {
+      states > gdn::kMaxWindowStates ||
+      !gdn::aligned16(projected, dynamic_scale, scales, compensator_keys, compensator_values,
+                      record_decay, record_keys, record_corrections, positions, decay,
+                      write_keys, reads, queries, values, outputs)) {
     return gdn::kStatusInvalidArgument;
   }
   const gdn::VectorArgs in{write_keys, reads, queries, decay, nullptr, states, false};
@@ -763,7 +770,10 @@ extern "C" int32_t statecentric_gdn_state_codec_finish_decode_pair_bf16_launch_v
   if (!projected || !dynamic_scale || !scales || !compensator_keys || !compensator_values ||
       !record_decay || !record_keys || !record_corrections || !positions || !decay ||
       !beta || !keys || !queries || !values || !outputs || states == 0 ||
-      states > gdn::kMaxWindowStates || states % 2 != 0) {
+      states > gdn::kMaxWindowStates || states % 2 != 0 ||
+      !gdn::aligned16(projected, dynamic_scale, scales, compensator_keys, compensator_values,
+                      record_decay, record_keys, record_corrections, positions, decay, beta,
+                      keys, queries, values, outputs)) {
     return gdn::kStatusInvalidArgument;
   }
   const gdn::VectorArgs in{keys, nullptr, queries, decay, beta, states, true};

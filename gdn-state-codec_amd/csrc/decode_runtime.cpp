@@ -59,7 +59,10 @@ extern "C" int32_t statecentric_gdn_state_codec_decode_runtime_step_v1(
   {
     std::lock_guard<std::mutex> lock(runtime_mutex);
     auto* runtime = static_cast<DecodeRuntime*>(opaque);
-    if (runtime == nullptr || runtime != shared_runtime || states != runtime->states) {
+    if (runtime == nullptr || runtime != shared_runtime || states != runtime->states ||
+        !gdn::aligned16(residual, smoothing, scales, compensator_keys, compensator_values,
+                        record_decay, record_keys, record_corrections, positions, decay, beta,
+                        keys, queries, values, outputs)) {
       return 1;
     }
   }

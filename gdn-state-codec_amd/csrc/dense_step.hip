@@ -62,7 +62,8 @@ extern "C" int32_t statecentric_gdn_state_codec_fp32_gdn_step_launch_v1(
     const uint16_t* reads, const uint16_t* queries, const uint16_t* values, float* outputs,
     uint32_t states) {
   if (!dense_state || !decay || !write_keys || !reads || !queries || !values || !outputs ||
-      states == 0 || states > gdn::kMaxWindowStates) {
+      states == 0 || states > gdn::kMaxWindowStates ||
+      !gdn::aligned16(dense_state, decay, write_keys, reads, queries, values, outputs)) {
     return gdn::kStatusInvalidArgument;
   }
   const dim3 grid((states + gdn::kStatesPerBlock - 1) / gdn::kStatesPerBlock);

@@ -33,6 +33,18 @@ constexpr uint32_t kDtypeBF16 = 1;
 // Largest grid the launchers issue along x (hardware limit 2^31 - 1).
 constexpr uint64_t kMaxGrid = 0x7FFFFFFFull;
 
+// Every device pointer an entry point takes must be 16-byte aligned.  The
+// kernels move codes and fp32 tiles as 16-byte vectors and narrower words at
+// offsets that are multiples of their own width, so a 16-byte aligned base
+// keeps every access aligned.  Allocations (hipMalloc, torch) are 256-byte
+// aligned; a view that starts at an arbitrary element offset may not be, and
+// the entry points reject it with status 1 before any launch.  Null pointers
+// pass this test (they are rejected separately where they are not allowed).
+template <typename... Pointers>
+inline bool aligned16(const Pointers*... pointers) {
+  return ((reinterpret_cast<uintptr_t>(pointers) % 16u == 0u) && ...);
+}
+
 // Launches `kernel` on `stream` through hipLaunchKernel so the launch status
 // comes back to the caller instead of staying in the thread's last-error slot.
 // Arguments are converted to the kernel's parameter types first.

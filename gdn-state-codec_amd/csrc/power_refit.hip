@@ -418,7 +418,11 @@ extern "C" int32_t statecentric_gdn_state_codec_window_boundary_noalloc_launch_v
       !record_decay || !record_keys || !record_corrections || !positions || !next_residual ||
       !next_smoothing || !next_scales || !next_compensator_keys || !next_compensator_values ||
       states == 0 || states > gdn::kMaxWindowStates || power_iterations > 32 ||
-      (power_iterations > 0 && states > gdn::kNoAllocMaxStates)) {
+      (power_iterations > 0 && states > gdn::kNoAllocMaxStates) ||
+      !gdn::aligned16(residual, smoothing, scales, compensator_keys, compensator_values,
+                      record_decay, record_keys, record_corrections, positions, next_residual,
+                      next_smoothing, next_scales, next_compensator_keys,
+                      next_compensator_values)) {
     return gdn::kStatusInvalidArgument;
   }
   if (power_iterations == 0) {  // the quant-only refit uses no workspace

@@ -355,7 +355,8 @@ statecentric_gdn_state_codec_encoded_projection_decode_launch_v4(
   if (residual == nullptr || smoothing == nullptr || scales == nullptr ||
       queries == nullptr || outputs == nullptr || batch == 0 ||
       !gdn::projection_shape_ok(value_heads, query_heads) ||
-      (layout != gdn::kKeyValue && layout != gdn::kValueKey)) {
+      (layout != gdn::kKeyValue && layout != gdn::kValueKey) ||
+      !gdn::aligned16(residual, smoothing, scales, queries, outputs)) {
     return gdn::kStatusInvalidArgument;
   }
   const uint64_t tiles = static_cast<uint64_t>(batch) * value_heads;
@@ -386,7 +387,8 @@ statecentric_gdn_state_codec_encoded_projection_chunked_launch_v4(
   if (residual == nullptr || smoothing == nullptr || scales == nullptr ||
       queries == nullptr || outputs == nullptr || seqs == 0 || tokens == 0 ||
       !gdn::projection_shape_ok(value_heads, query_heads) ||
-      (layout != gdn::kKeyValue && layout != gdn::kValueKey)) {
+      (layout != gdn::kKeyValue && layout != gdn::kValueKey) ||
+      !gdn::aligned16(residual, smoothing, scales, queries, outputs)) {
     return gdn::kStatusInvalidArgument;
   }
   const uint64_t pairs = static_cast<uint64_t>(seqs) * value_heads;

@@ -421,7 +421,10 @@ extern "C" int32_t statecentric_gdn_state_codec_windowed_gdn_step_launch_v1(
       !compensator_values || !record_decay || !record_keys ||
       !record_corrections || !positions || !decay || !write_keys || !reads ||
       !queries || !values || !outputs || states == 0 ||
-      states > gdn::kMaxWindowStates) {
+      states > gdn::kMaxWindowStates ||
+      !gdn::aligned16(residual, smoothing, scales, compensator_keys, compensator_values,
+                      record_decay, record_keys, record_corrections, positions, decay,
+                      write_keys, reads, queries, values, outputs)) {
     return gdn::kStatusInvalidArgument;
   }
   const StepArgs args{residual, smoothing, scales, compensator_keys,
@@ -445,7 +448,10 @@ int32_t bf16_step(void* stream, const int8_t* residual, const float* smoothing,
       !compensator_values || !record_decay || !record_keys ||
       !record_corrections || !positions || !decay || !beta || !keys ||
       !queries || !values || !outputs || states == 0 ||
-      states > gdn::kMaxWindowStates || states % 2 != 0) {
+      states > gdn::kMaxWindowStates || states % 2 != 0 ||
+      !gdn::aligned16(residual, smoothing, scales, compensator_keys, compensator_values,
+                      record_decay, record_keys, record_corrections, positions, decay, beta,
+                      keys, queries, values, outputs)) {
     return gdn::kStatusInvalidArgument;
   }
   const StepArgs args{residual, smoothing, scales, compensator_keys,

@@ -24,6 +24,9 @@
  * No counterpart exists on the reference's device side: the reference
  * serializes one CPU capsule at a time (state_capsule.cpp:446-578); these
  * entry points replace that pair for a whole batch of slots.
+ *
+ * Alignment: every device pointer argument must be 16-byte aligned (see
+ * gdn_state_codec_kernel.h); a misaligned pointer returns 1 before any launch.
  */
 #ifndef GDN_STATE_CODEC_CAPSULE_H
 #define GDN_STATE_CODEC_CAPSULE_H

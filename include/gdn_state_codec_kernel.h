@@ -9,6 +9,11 @@
  * out-of-range count/enum (the reference's status 1), 5 when HIP rejects the
  * launch.
  *
+ * Alignment: every device pointer argument must be 16-byte aligned (the
+ * kernels move tiles as 16-byte vectors).  hipMalloc and torch allocations are
+ * 256-byte aligned, and so is every per-tile view of them; a view that starts
+ * at an arbitrary element offset may not be, and returns 1 before any launch.
+ *
  * Numerics: codes, smoothing and scales are bit-identical to the reference's
  * portable C++ QuantizeBoundary quant stage (quant-only initializer) and dense
  * outputs to its DequantizeBoundary:

@@ -16,6 +16,9 @@
  *
  * Same conventions as gdn_state_codec_kernel.h: asynchronous on `stream`, no
  * allocation, status 0 / 1 (bad argument) / 5 (launch failed).
+ *
+ * Alignment: every device pointer argument must be 16-byte aligned (see
+ * gdn_state_codec_kernel.h); a misaligned pointer returns 1 before any launch.
  */
 #ifndef GDN_STATE_CODEC_PROJECTION_H
 #define GDN_STATE_CODEC_PROJECTION_H

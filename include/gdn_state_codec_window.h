@@ -31,6 +31,10 @@
  * Every entry point is asynchronous on `stream` (NULL = HIP's null stream) and
  * returns 0 on success, 1 for a null pointer or an out-of-range count (the
  * reference's status 1), 5 when HIP rejects a launch.
+ *
+ * Alignment: every device pointer argument must be 16-byte aligned (see
+ * gdn_state_codec_kernel.h); a misaligned pointer returns 1 before any launch
+ * (the runtime steps too, ahead of their per-stage statuses).
  */
 #ifndef GDN_STATE_CODEC_WINDOW_H
 #define GDN_STATE_CODEC_WINDOW_H

@@ -236,3 +236,74 @@ def test_capsule_entry_points_admit_and_size_capsules(lib):
         for geometry in (b"A" * 64, b"0123456789abcdeg" + b"0" * 48, None):
             assert fn(geometry=geometry) == 1
         assert fn(generation=0) == 1 and fn(epoch=0) == 1
+
+
+# Argument templates of every entry point with valid counts: "P" marks a device
+# pointer the kernels access (it must be 16-byte aligned), other entries are
+# passed as written (the stream, host pointers, unused Cube workspace/tiling).
+_GEOMETRY = b"0123456789abcdef" * 4
+_ALIGNMENT_CASES = {
+    "smoothing_launch_v1": [None, "P", "P"],
+    "quantize_launch_v1": [None] + ["P"] * 4,
+    "dequantize_launch_v1": [None] + ["P"] * 6,
+    "provider_smoothing_launch_v2": [None, "P", "P", 4],
+    "provider_quantize_launch_v2": [None] + ["P"] * 4 + [4],
+    "provider_initialize_launch_v3": [None] + ["P"] * 4 + [4],
+    "encode_launch_v4": [None] + ["P"] * 4 + [4, 0],
+    "decode_launch_v4": [None] + ["P"] * 6 + [4, 0],
+    "pool_encode_launch_v4": [None, "P", 0, "P", 2, 1, 4, 2, 0, "P", "P", "P"],
+    "pool_decode_launch_v4": [None, "P", "P", "P", "P", 2, 1, 4, 2, 0, "P", 0],
+    "encoded_projection_decode_launch_v4": [None] + ["P"] * 5 + [1, 32, 16, 1.0, 1],
+    "encoded_projection_chunked_launch_v4": [None] + ["P"] * 5 + [1, 4, 32, 16, 1.0, 1],
+    "windowed_gdn_step_launch_v1": [None] + ["P"] * 15 + [2],
+    "windowed_gdn_step_bf16_launch_v1": [None] + ["P"] * 15 + [2],
+    "windowed_gdn_step_bf16_quant_only_launch_v1": [None] + ["P"] * 15 + [2],
+    "fp32_gdn_step_launch_v1": [None] + ["P"] * 7 + [2],
+    "prepare_int8_vector_launch_v1": [None] + ["P"] * 4 + [2],
+    "prepare_decode_pair_launch_v1": [None] + ["P"] * 6 + [2],
+    "prepare_decode_pair_bf16_launch_v1": [None] + ["P"] * 6 + [2],
+    "int8_cube_matmul_launch_v1": [None, "P", "P", "P", 2, 0, 16, 16, 1],
+    "finish_decode_pair_launch_v1": [None] + ["P"] * 15 + [2],
+    "finish_decode_pair_bf16_launch_v1": [None] + ["P"] * 15 + [2],
+    "window_boundary_launch_v1": [None] + ["P"] * 15 + [2, 0],
+    "window_boundary_noalloc_launch_v1": [None] + ["P"] * 14 + [2, 4],
+    "boundary_scale_records_launch_v1": [None] + ["P"] * 3 + [2],
+    "window_boundary_cube_finish_launch_v1": [None] + ["P"] * 15 + [2],
+    "bf16_cube_matmul_launch_v1": [None, "P", "P", "P", 2, 16, 16, 1],
+    "capsule_serialize_launch_v1": [None] + ["P"] * 9 + [1, _GEOMETRY, 1, 1, "P", "P", 1 << 20,
+                                                          "P", 2],
+    "capsule_restore_launch_v1": [None, "P", "P", "P", 1 << 20, _GEOMETRY, 1, 1, "P", 1]
+                                 + ["P"] * 10 + [2],
+}
+
+
+@pytest.mark.parametrize("name", sorted(_ALIGNMENT_CASES))
+def test_misaligned_pointers_return_status_1(lib, name):
+    """Each device pointer in turn 4 bytes off a 16-byte boundary, every other
+    argument valid: status 1, before any HIP call (this runs without a GPU)."""
+    template = _ALIGNMENT_CASES[name]
+    fn = getattr(lib, name)
+    slots = [i for i, a in enumerate(template) if a == "P"]
+    assert slots and len(template) == len(fn.argtypes), name
+    for slot in slots:
+        args = [ctypes.c_void_p(20 if i == slot else 16) if a == "P" else a
+                for i, a in enumerate(template)]
+        assert fn(*args) == 1, (name, slot)
+
+
+def test_runtime_steps_reject_misaligned_pointers(lib):
+    """The decode and boundary runtime steps: a misaligned pointer is a bad
+    argument (status 1), whatever stage it belongs to."""
+    decode = lib.decode_runtime_create_v1(2)
+    boundary = lib.boundary_runtime_create_v1(2)
+    assert decode and boundary
+    try:
+        for slot in range(15):
+            args = [ctypes.c_void_p(20 if i == slot else 16) for i in range(15)]
+            assert lib.decode_runtime_step_v1(decode, None, *args, 2) == 1, slot
+        for slot in range(5):
+            args = [ctypes.c_void_p(20 if i == slot else 16) for i in range(5)]
+            assert lib.boundary_runtime_step_v1(boundary, None, *args, 2) == 1, slot
+    finally:
+        lib.decode_runtime_destroy_v1(decode)
+        lib.boundary_runtime_destroy_v1(boundary)
