@@ -175,10 +175,31 @@ def _c1_style_state(shape, gen, dev):
     return torch.where(mask, signs, x)
 
 
+def _time_back_to_back(fn, calls, steps: int) -> float:
+    """Microseconds per launch of `fn` over back-to-back launches cycling
+    through the argument tuples `calls` (one per rotated state copy), between
+    one event pair: the per-step time of a loop issuing one projection after
+    another.  The entry point is called with prepared arguments so that the
+    host keeps ahead of the GPU.  A warm phase of the same launches (at least
+    400, about 10 ms) first brings the GPU to its sustained clocks, which a
+    short timed region right after an idle host-side phase would not see."""
+    import torch
+
+    for i in range(400):
+        assert fn(*calls[i % len(calls)]) == 0
+    n = max(steps * len(calls), 400)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(n):
+        fn(*calls[i % len(calls)])
+    b.record()
+    return _events_ms([(a, b)])[0] / n * 1e3
+
+
 def bench_decode_projection(steps: int, warmup: int):
     import torch
 
-    from gdn_state_codec import codec
+    from gdn_state_codec import codec, native
 
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
@@ -192,19 +213,14 @@ def bench_decode_projection(steps: int, warmup: int):
         out = torch.empty((256, 32, 128), dtype=torch.float32, device=dev)
         sets.append((c, s, sc, q, out))
         del x
-    for i in range(warmup * ROTATIONS):
+    for i in range(warmup * ROTATIONS):  # validated calls: shapes, dtypes, devices
         c, s, sc, q, out = sets[i % ROTATIONS]
         codec.project_decode(c, s, sc, q, 1.0, codec.LAYOUT_VALUE_KEY, out)
-    # Back-to-back launches between one event pair: the per-step time of a
-    # decode loop that issues one projection after another.
-    n = max(steps, 4) * ROTATIONS
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for i in range(n):  # the warmup validated these buffers
-        c, s, sc, q, out = sets[i % ROTATIONS]
-        codec.project_decode(c, s, sc, q, 1.0, codec.LAYOUT_VALUE_KEY, out, validate=False)
-    b.record()
-    us = _events_ms([(a, b)])[0] / n * 1e3
+    fn = native().encoded_projection_decode_launch_v4
+    stream = torch.cuda.current_stream().cuda_stream
+    calls = [(stream, c.data_ptr(), s.data_ptr(), sc.data_ptr(), q.data_ptr(), out.data_ptr(),
+              256, 32, 16, 1.0, codec.LAYOUT_VALUE_KEY) for c, s, sc, q, out in sets]
+    us = _time_back_to_back(fn, calls, steps)
     _log(f"config 3: decode projection {us:.2f} us/step")
     return us, sets[0]
 
@@ -212,7 +228,7 @@ def bench_decode_projection(steps: int, warmup: int):
 def bench_chunked_projection(steps: int, warmup: int):
     import torch
 
-    from gdn_state_codec import codec
+    from gdn_state_codec import codec, native
 
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
@@ -225,17 +241,14 @@ def bench_chunked_projection(steps: int, warmup: int):
         out = torch.empty((64, 64, 32, 128), dtype=torch.float32, device=dev)
         sets.append((c, s, sc, q, out))
         del x
-    for i in range(warmup * ROTATIONS):
+    for i in range(warmup * ROTATIONS):  # validated calls: shapes, dtypes, devices
         c, s, sc, q, out = sets[i % ROTATIONS]
         codec.project_chunked(c, s, sc, q, 1.0, codec.LAYOUT_VALUE_KEY, out)
-    n = max(steps, 4) * ROTATIONS
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for i in range(n):  # the warmup validated these buffers
-        c, s, sc, q, out = sets[i % ROTATIONS]
-        codec.project_chunked(c, s, sc, q, 1.0, codec.LAYOUT_VALUE_KEY, out, validate=False)
-    b.record()
-    us = _events_ms([(a, b)])[0] / n * 1e3
+    fn = native().encoded_projection_chunked_launch_v4
+    stream = torch.cuda.current_stream().cuda_stream
+    calls = [(stream, c.data_ptr(), s.data_ptr(), sc.data_ptr(), q.data_ptr(), out.data_ptr(),
+              64, 64, 32, 32, 1.0, codec.LAYOUT_VALUE_KEY) for c, s, sc, q, out in sets]
+    us = _time_back_to_back(fn, calls, steps)
     _log(f"config 4: chunked projection {us:.2f} us/step")
     return us, sets[0]
 
