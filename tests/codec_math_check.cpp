@@ -7,6 +7,13 @@
 //   codec_math_check divrandom N     N random divisors b in [2^-90, 2^90] x every
 //                                    significand of a, exponents chosen so that
 //                                    2^-120 <= |a/b| <= 2^120
+//   codec_math_check refit           the quant-only refit's fast domain: divisors s
+//                                    in [2^-20, 2^20] at its edges and around 1
+//                                    (exponents -20, -19, -1, 0, 1, 19 with a
+//                                    power-of-two, an all-ones and two random
+//                                    significands, and s = 2^20) x every significand
+//                                    of dividends at the domain's edges (|w| in
+//                                    [2^-100, 2^-99) and [2^99, 2^100], both signs)
 //   codec_math_check round           every float |x| <= 127: round_half_away_small(x)
 //                                    == clamp(lroundf(x), -127, 127)
 // Prints "<checked> <failures>" and exits non-zero on any failure.
@@ -92,6 +99,37 @@ void check_div_random(int divisors) {
   }
 }
 
+void check_refit_domain() {
+  std::vector<float> divisors;
+  srand(20261202);
+  for (int e : {-20, -19, -1, 0, 1, 19}) {
+    const uint32_t exponent = static_cast<uint32_t>(e + 127) << 23;
+    for (uint32_t mantissa : {0u, 0x7FFFFFu,
+                              ((static_cast<uint32_t>(rand()) << 12) ^ rand()) & 0x7FFFFFu,
+                              ((static_cast<uint32_t>(rand()) << 12) ^ rand()) & 0x7FFFFFu}) {
+      divisors.push_back(from_bits(exponent | mantissa));
+    }
+  }
+  divisors.push_back(1048576.0f);  // s = 2^20, the top of the domain
+  for (const float b : divisors) {
+    const float y = 1.0f / b;
+    // |w| in [2^-100, 2^-99) and [2^99, 2^100): every significand, both signs.
+    for (const uint32_t biased : {27u, 226u}) {
+      parallel(0, 1u << 23, [&](uint64_t m, uint64_t& n, uint64_t& bad) {
+        for (uint32_t sign = 0; sign < 2; ++sign) {
+          const float a = from_bits((sign << 31) | (biased << 23) | static_cast<uint32_t>(m));
+          ++n;
+          if (to_bits(gdn::div_by_reciprocal(a, b, y)) != to_bits(a / b)) ++bad;
+        }
+      });
+    }
+    for (const float a : {0x1p100f, -0x1p100f}) {  // the top edge itself
+      ++checked;
+      if (to_bits(gdn::div_by_reciprocal(a, b, y)) != to_bits(a / b)) ++failures;
+    }
+  }
+}
+
 void check_round() {
   const uint64_t end = static_cast<uint64_t>(to_bits(127.0f)) + 1;
   parallel(0, end, [&](uint64_t u, uint64_t& n, uint64_t& bad) {
@@ -114,6 +152,8 @@ int main(int argc, char** argv) {
     check_div127();
   } else if (strcmp(argv[1], "divrandom") == 0) {
     check_div_random(argc > 2 ? atoi(argv[2]) : 64);
+  } else if (strcmp(argv[1], "refit") == 0) {
+    check_refit_domain();
   } else if (strcmp(argv[1], "round") == 0) {
     check_round();
   } else {

@@ -50,6 +50,15 @@ def test_division_by_random_divisors_is_ieee(checker):
     assert checked == 48 * 2 * (1 << 23) and failures == 0 and rc == 0
 
 
+def test_refit_division_is_ieee_at_the_edges_of_its_fast_domain(checker):
+    """The quant-only refit divides w / s by the reciprocal of the smoothing
+    value when s is in [2^-20, 2^20] and w is 0 or in [2^-100, 2^100]
+    (csrc/boundary.hip): divisors at the domain's edges, with power-of-two and
+    all-ones significands, against every dividend significand at its edges."""
+    rc, checked, failures = _run(checker, "refit")
+    assert checked == 25 * (2 * 2 * (1 << 23) + 2) and failures == 0 and rc == 0
+
+
 def test_rounding_matches_lround_for_every_float_up_to_127(checker):
     rc, checked, failures = _run(checker, "round")
     assert checked > 2_000_000_000 and failures == 0 and rc == 0
