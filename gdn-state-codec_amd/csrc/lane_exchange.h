@@ -75,6 +75,42 @@ __device__ __forceinline__ T fold(T lo, T hi, int lane) {
   }
 }
 
+// fold with fmaxf in place of the sum: a lane with the bit clear ends with
+// max(lo, partner's lo), a lane with the bit set with max(hi, partner's hi).
+template <int kMask>
+__device__ __forceinline__ float fold_max(float lo, float hi, int lane) {
+  if constexpr (kMask == 16 || kMask == 32) {
+    const auto r = kMask == 32
+        ? __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, lo),
+                                           __builtin_bit_cast(uint32_t, hi), false, false)
+        : __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, lo),
+                                           __builtin_bit_cast(uint32_t, hi), false, false);
+    const uint32_t first = r[0];
+    const uint32_t second = r[1];
+    return fmaxf(__builtin_bit_cast(float, first), __builtin_bit_cast(float, second));
+  } else {
+    const bool up = (lane & kMask) != 0;
+    const float send = up ? lo : hi;
+    const float keep = up ? hi : lo;
+    return fmaxf(keep, from_lane_xor<kMask>(send));
+  }
+}
+
+// max(x, x of lane ^ kMask), the same value in both lanes of a pair.
+template <int kMask>
+__device__ __forceinline__ float max_partner(float x) {
+  if constexpr (kMask == 16 || kMask == 32) {
+    const uint32_t bits = __builtin_bit_cast(uint32_t, x);
+    const auto r = kMask == 32 ? __builtin_amdgcn_permlane32_swap(bits, bits, false, false)
+                               : __builtin_amdgcn_permlane16_swap(bits, bits, false, false);
+    const uint32_t first = r[0];
+    const uint32_t second = r[1];
+    return fmaxf(__builtin_bit_cast(float, first), __builtin_bit_cast(float, second));
+  } else {
+    return fmaxf(x, from_lane_xor<kMask>(x));
+  }
+}
+
 // x + (x of lane ^ kMask), the same value in both lanes of a pair.
 template <int kMask>
 __device__ __forceinline__ float add_partner(float x) {

@@ -18,15 +18,18 @@
 // state, operands staged in LDS: the codes at a 132-byte row stride so both
 // the row walk and the column walk are free of bank conflicts, compensators
 // and records as fp16 bits, and a 256-entry table of code / 127.  The fitted
-// residual is evaluated once per cell into the workspace, which the smoothing,
-// scale and code passes then read back.
+// residual is evaluated once per cell, one key row per thread held in
+// registers for the smoothing, scale and code passes, and written once to the
+// workspace.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "codec_math.h"
 #include "gdn_state_codec_window.h"
+#include "lane_exchange.h"
 #include "launch.h"
 #include "window_common.h"
 
@@ -36,6 +39,17 @@ namespace {
 constexpr int kThreads = 128;
 constexpr int kCodeStride = kDim + 4;
 constexpr float kBoundaryFloor = 1.0e-8f;
+
+// f(std::integral_constant<int, c>) for c = 0 .. kDim - 1, expanded at compile
+// time: a body that indexes a register array by c keeps the array in VGPRs,
+// where a loop the compiler declines to unroll fully would move it to scratch.
+template <int kColumn = 0, typename F>
+__device__ __forceinline__ void each_column(F&& f) {
+  if constexpr (kColumn < kDim) {
+    f(std::integral_constant<int, kColumn>{});
+    each_column<kColumn + 1>(f);
+  }
+}
 
 struct PowerArgs {
   const int8_t* residual;
@@ -63,7 +77,12 @@ struct PowerShared {
   int8_t code[kDim * kCodeStride];  // [value column][key row]
   uint16_t ck[kDim * kRank], cv[kDim * kRank];
   uint16_t nk[kDim * kRank], nv[kDim * kRank];
-  uint16_t rk[kWindow * kDim], rc[kWindow * kDim];
+  // Records as [dimension][record]: a dimension's 16 records are 32
+  // contiguous bytes, so the record projections (lane j walks record j)
+  // read consecutive words and a cell reads its 16 records as two 16-byte
+  // words.
+  alignas(16) uint16_t rk[kDim * kWindow];
+  alignas(16) uint16_t rc[kDim * kWindow];
   float smoothing[kDim], scales[kDim];
   union {
     float left[kDim];            // power iteration
@@ -140,7 +159,7 @@ __device__ void projections(PowerShared& sh, const float* vector, const uint16_t
   } else if (t >= 64 && t < 64 + kWindow) {
     const int j = t - 64;
     float acc = 0.0f;
-    for (int i = 0; i < kDim; ++i) acc += h2f(record_basis[j * kDim + i]) * vector[i];
+    for (int i = 0; i < kDim; ++i) acc += h2f(record_basis[i * kWindow + j]) * vector[i];
     sh.record_projection[j] = acc;
   }
   __syncthreads();
@@ -159,7 +178,7 @@ __device__ void apply_right(PowerShared& sh, const float* vector, float* output,
   }
   for (int r = 0; r < kRank; ++r) value += h2f(sh.ck[row * kRank + r]) * sh.old_projection[r] * bs;
   for (int j = 0; j < kWindow; ++j) {
-    value += h2f(sh.rk[j * kDim + row]) * sh.record_projection[j] * sh.record_suffix[j];
+    value += h2f(sh.rk[row * kWindow + j]) * sh.record_projection[j] * sh.record_suffix[j];
   }
   for (int r = 0; r < fitted; ++r) value -= h2f(sh.nk[row * kRank + r]) * sh.fitted_projection[r];
   __syncthreads();  // every thread has read `vector` before it may be overwritten
@@ -180,7 +199,7 @@ __device__ void apply_transpose(PowerShared& sh, const float* vector, float* out
   }
   for (int r = 0; r < kRank; ++r) value += h2f(sh.cv[column * kRank + r]) * sh.old_projection[r] * bs;
   for (int j = 0; j < kWindow; ++j) {
-    value += h2f(sh.rc[j * kDim + column]) * sh.record_projection[j] * sh.record_suffix[j];
+    value += h2f(sh.rc[column * kWindow + j]) * sh.record_projection[j] * sh.record_suffix[j];
   }
   for (int r = 0; r < fitted; ++r) value -= h2f(sh.nv[column * kRank + r]) * sh.fitted_projection[r];
   __syncthreads();
@@ -188,22 +207,7 @@ __device__ void apply_transpose(PowerShared& sh, const float* vector, float* out
   __syncthreads();
 }
 
-// ResidualCell (:223-251).
-__device__ __forceinline__ float residual_cell(const PowerShared& sh, int row, int column,
-                                               float bs) {
-  float value = code_value(sh, sh.code[column * kCodeStride + row]) * sh.smoothing[row] *
-                sh.scales[column] * bs;
-  for (int r = 0; r < kRank; ++r) {
-    value += h2f(sh.ck[row * kRank + r]) * h2f(sh.cv[column * kRank + r]) * bs;
-    value -= h2f(sh.nk[row * kRank + r]) * h2f(sh.nv[column * kRank + r]);
-  }
-  for (int j = 0; j < kWindow; ++j) {
-    value += h2f(sh.rk[j * kDim + row]) * h2f(sh.rc[j * kDim + column]) * sh.record_suffix[j];
-  }
-  return value;
-}
-
-__global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void power_refit_kernel(PowerArgs a) {
   extern __shared__ __align__(16) unsigned char dynamic[];
   PowerShared& sh = *reinterpret_cast<PowerShared*>(dynamic);
   const int t = threadIdx.x;
@@ -225,11 +229,12 @@ __global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
     sh.nv[i] = 0u;
   }
   for (int i = t; i < kWindow * kDim; i += kThreads) {
-    sh.rk[i] = a.record_keys[rb * kDim + i];
-    sh.rc[i] = a.record_corrections[rb * kDim + i];
+    const int j = i / kDim, dimension = i % kDim;
+    sh.rk[dimension * kWindow + j] = a.record_keys[rb * kDim + i];
+    sh.rc[dimension * kWindow + j] = a.record_corrections[rb * kDim + i];
   }
-  sh.smoothing[t] = a.smoothing[vb + t];
-  sh.scales[t] = a.scales[vb + t];
+  sh.smoothing[t] = (a.smoothing + vb)[t];
+  sh.scales[t] = (a.scales + vb)[t];
   sh.code_value[t] = code_over_127(static_cast<int8_t>(t));
   sh.code_value[t + kThreads] = code_over_127(static_cast<int8_t>(t + kThreads));
   // BuildSuffix (:102-111), computed identically by every thread.
@@ -238,6 +243,8 @@ __global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
     if (t == 0) sh.record_suffix[j] = bs;
     bs *= a.record_decay[rb + j];
   }
+  // The same value in every lane: keep it in a scalar register.
+  bs = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bs)));
   __syncthreads();
 
   // ---- deflated power iteration ---------------------------------------------
@@ -267,60 +274,144 @@ __global__ __launch_bounds__(kThreads) void power_refit_kernel(PowerArgs a) {
     __syncthreads();
   }
 
-  // ---- residual (column t) into the workspace ---------------------------------
-  // Each cell of R minus the fit is evaluated once, stored coalesced (lanes
-  // hold consecutive values), and read back by the three passes that follow;
-  // the reads return the same fp32 bits the evaluation would.
-  float* const work = a.workspace + state * kTile;  // [key row][value column]
+  // ---- R minus the fit: row t in registers, and into the workspace ----------
+  // Thread t owns key row t: its 128 fitted cells stay in registers through
+  // the smoothing, scale and code passes, so the workspace is written once
+  // and never read back.  Each cell is the reference's ResidualCell
+  // (:223-251), evaluated in its order.  The column loops are unrolled at
+  // compile time (each_column) so that cell[] is only ever indexed by
+  // constants and lives in VGPRs.
+  const int row = t;
+  float cell[kDim];
   {
-    const int column = t;
-    for (int row = 0; row < kDim; ++row) {
-      work[row * kDim + column] = residual_cell(sh, row, column, bs);
+    // The row's operands stay as fp16 pairs (widened where used) and the
+    // window suffix products, the same for every thread, in scalar
+    // registers, leaving the vector registers to the cells.
+    const float s = sh.smoothing[row];
+    uint32_t ck2[kRank / 2], nk2[kRank / 2], rk2[kWindow / 2];
+    float suffix[kWindow];
+#pragma unroll
+    for (int i = 0; i < kRank / 2; ++i) {
+      ck2[i] = reinterpret_cast<const uint32_t*>(sh.ck + row * kRank)[i];
+      nk2[i] = reinterpret_cast<const uint32_t*>(sh.nk + row * kRank)[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kWindow / 2; ++i) rk2[i] = reinterpret_cast<const uint32_t*>(sh.rk + row * kWindow)[i];
+#pragma unroll
+    for (int j = 0; j < kWindow; ++j) {
+      suffix[j] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sh.record_suffix[j])));
+    }
+    const auto low = [](uint32_t pair, int i) { return h2f(i & 1 ? pair >> 16 : pair & 0xFFFFu); };
+    each_column([&](auto c) {
+      constexpr int column = decltype(c)::value;
+      // Opaque to the compiler, so the pairs are widened per column instead of
+      // once into 24 long-lived registers.
+#pragma unroll
+      for (int i = 0; i < kRank / 2; ++i) asm volatile("" : "+v"(ck2[i]), "+v"(nk2[i]));
+#pragma unroll
+      for (int i = 0; i < kWindow / 2; ++i) asm volatile("" : "+v"(rk2[i]));
+      float value = code_value(sh, sh.code[column * kCodeStride + row]) * s *
+                    sh.scales[column] * bs;
+#pragma unroll
+      for (int r = 0; r < kRank; ++r) {
+        value += low(ck2[r / 2], r) * h2f(sh.cv[column * kRank + r]) * bs;
+        value -= low(nk2[r / 2], r) * h2f(sh.nv[column * kRank + r]);
+      }
+      const uint4* const rc4 = reinterpret_cast<const uint4*>(sh.rc + column * kWindow);
+      const uint4 c0 = rc4[0], c1 = rc4[1];
+      const uint32_t rc2[kWindow / 2] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+      for (int j = 0; j < kWindow; ++j) {
+        value += low(rk2[j / 2], j) * low(rc2[j / 2], j) * suffix[j];
+      }
+      cell[column] = value;
+      // One column's operands at a time: the scheduler would otherwise hoist
+      // the LDS reads of many columns ahead of their use.
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+  {
+    float4* const work = reinterpret_cast<float4*>((a.workspace + state * kTile) + row * kDim);
+#pragma unroll
+    for (int q = 0; q < kDim / 4; ++q) {
+      work[q] = make_float4(cell[4 * q], cell[4 * q + 1], cell[4 * q + 2], cell[4 * q + 3]);
     }
   }
-  __syncthreads();  // the workspace writes are visible to the whole workgroup
 
   // ---- fresh smoothing (row t): sequential sum of |cell| over the columns ----
+  float s_new;
   {
-    const int row = t;
-    const float4* cells = reinterpret_cast<const float4*>(work + row * kDim);
     float mean_absolute = 0.0f;
-    for (int q = 0; q < kDim / 4; ++q) {
-      const float4 c = cells[q];
-      mean_absolute += fabsf(c.x);
-      mean_absolute += fabsf(c.y);
-      mean_absolute += fabsf(c.z);
-      mean_absolute += fabsf(c.w);
-    }
+    each_column([&](auto c) { mean_absolute += fabsf(cell[decltype(c)::value]); });
     const float mean = mean_absolute / 128.0f;
-    const float s = newton_sqrt(mean > kBoundaryFloor ? mean : kBoundaryFloor);
-    sh.next_smoothing[row] = s;
-    a.next_smoothing[vb + row] = s;
+    s_new = newton_sqrt(mean > kBoundaryFloor ? mean : kBoundaryFloor);
+    (a.next_smoothing + vb)[row] = s_new;
+  }
+  // m = cell / s_new is formed where it is used (the scale and code passes
+  // each divide again, to the same bits) rather than stored over the cells.
+
+  // ---- scales: max over rows of |cell / s| per column -------------------------
+  // The reference keeps `value > maximum ? value : maximum` from 0 over the
+  // rows, which skips NaNs; fmaxf(|m|, 0) maps a NaN to 0 and leaves every
+  // other |m| alone, and a maximum of those is exact in any order.  Each
+  // wavefront reduces its 64 rows with quarter-width reduce-scatters (32
+  // columns across 64 lanes: lane L ends with column L % 32), then the two
+  // wavefronts' maxima meet in LDS.
+  const int lane = t & 63;
+  const int wave = t >> 6;
+#pragma unroll
+  for (int quarter = 0; quarter < 4; ++quarter) {
+    const auto magnitude = [&](int i) {
+      return fmaxf(fabsf(cell[32 * quarter + i] / s_new), 0.0f);
+    };
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float lo = fold_max<16>(magnitude(i), magnitude(16 + i), lane);
+      const float hi = fold_max<16>(magnitude(8 + i), magnitude(24 + i), lane);
+      v[i] = fold_max<8>(lo, hi, lane);
+      if (i % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = fold_max<4>(v[i], v[i + 4], lane);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) v[i] = fold_max<2>(v[i], v[i + 2], lane);
+    v[0] = fold_max<1>(v[0], v[1], lane);
+    v[0] = max_partner<32>(v[0]);
+    if (lane < 32) {
+      (wave == 0 ? sh.left : sh.right)[32 * quarter + lane] = v[0];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __syncthreads();  // both wavefronts' column maxima; every cell has been evaluated
+  {
+    const float maximum = fmaxf(sh.left[t], sh.right[t]);
+    (a.next_scales + vb)[t] = maximum;
+    sh.left[t] = maximum;  // thread t's own slot: no other thread reads it yet
   }
   __syncthreads();
 
-  // ---- scales and codes (column t) ------------------------------------------
-  {
-    const int column = t;
-    float maximum = 0.0f;
-    for (int row = 0; row < kDim; ++row) {
-      const float value = fabsf(work[row * kDim + column] / sh.next_smoothing[row]);
-      maximum = value > maximum ? value : maximum;
-    }
-    a.next_scales[vb + column] = maximum;
-    int8_t* out = a.next_residual + state * kTile + static_cast<uint64_t>(column) * kDim;
-    for (int row4 = 0; row4 < kDim; row4 += 4) {
-      uint32_t packed = 0;
-      for (int i = 0; i < 4; ++i) {
-        const float smoothed = work[(row4 + i) * kDim + column] / sh.next_smoothing[row4 + i];
-        float q = maximum == 0.0f ? 0.0f : smoothed / maximum * 127.0f;
-        q += q >= 0.0f ? 0.5f : -0.5f;
-        q = q > 127.0f ? 127.0f : q;
-        q = q < -127.0f ? -127.0f : q;
-        packed |= (static_cast<uint32_t>(static_cast<int>(q)) & 0xFFu) << (8 * i);
-      }
-      *reinterpret_cast<uint32_t*>(out + row4) = packed;
-    }
+  // ---- codes: round-half-away (:336-345), staged in the code area ------------
+  each_column([&](auto c) {
+    constexpr int column = decltype(c)::value;
+    const float maximum = sh.left[column];
+    float q = maximum == 0.0f ? 0.0f : cell[column] / s_new / maximum * 127.0f;
+    q += q >= 0.0f ? 0.5f : -0.5f;
+    q = q > 127.0f ? 127.0f : q;
+    q = q < -127.0f ? -127.0f : q;
+    sh.code[column * kCodeStride + row] = static_cast<int8_t>(static_cast<int>(q));
+    if constexpr (column % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+  });
+  __syncthreads();
+  // next_residual [value column][key row]: each round of 16 columns, eight
+  // lanes write one whole 128-byte column.
+#pragma unroll
+  for (int round = 0; round < kDim / 16; ++round) {
+    const int column = 16 * round + (t >> 3);
+    const int offset = 16 * (t & 7);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&sh.code[column * kCodeStride + offset]);
+    *reinterpret_cast<uint4*>(a.next_residual + state * kTile + column * kDim + offset) =
+        make_uint4(src[0], src[1], src[2], src[3]);
   }
 
   // ---- new compensators, cleared window, position ----------------------------
