@@ -117,7 +117,41 @@ def _probe_library():
         getattr(lib, name).argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint64, ctypes.c_uint32]
         getattr(lib, name).restype = ctypes.c_int32
     lib.gdn_hbm_probe_grid.restype = ctypes.c_uint32
+    lib.gdn_valu_probe.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint32] * 3
+    lib.gdn_valu_probe.restype = ctypes.c_int32
     return lib
+
+
+def bench_valu_probe(repeats: int = 5):
+    """VALU issue ceiling of this GPU in wavefront instructions per second:
+    8192 workgroups of 4 wavefronts, each wavefront issuing 16 independent
+    operations per round for 2048 rounds (fp32 fma, u32 xor-add, fp64 add), no
+    memory traffic.  The figure that VALU-heavy kernels' SQ_INSTS_VALU rates
+    are compared with."""
+    import torch
+
+    lib = _probe_library()
+    dev = torch.device("cuda:0")
+    blocks, rounds = 8192, 2048
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    instructions = blocks * 4 * 16 * rounds
+    out = {}
+    for mode, name in ((0, "fma_f32"), (1, "xad_u32"), (2, "add_f64")):
+        for _ in range(2):
+            assert lib.gdn_valu_probe(stream, sink.data_ptr(), blocks, rounds, mode) == 0
+        pairs = []
+        for _ in range(repeats):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            assert lib.gdn_valu_probe(stream, sink.data_ptr(), blocks, rounds, mode) == 0
+            b.record()
+            pairs.append((a, b))
+        ms = sorted(_events_ms(pairs))[len(pairs) // 2]
+        out[f"{name}_Ginst_per_s"] = instructions / (ms * 1e-3) / 1e9
+    del sink
+    _log("valu probe: " + ", ".join(f"{k}={v:.0f}" for k, v in out.items()))
+    return out
 
 
 def bench_hbm_probe(repeats: int = 5):
@@ -164,6 +198,35 @@ def bench_hbm_probe(repeats: int = 5):
     del src, dst, sink
     _log("hbm probe: " + ", ".join(f"{k}={v:.0f}" for k, v in out.items()))
     return out
+
+
+def same_size_probe(kind: str, nbytes: int, steps: int) -> dict:
+    """The nontemporal probe `kind` ("read" or "copy") over a stream of the
+    size a projection step moves, timed like the projection legs: back-to-back
+    launches over ROTATIONS buffer copies (so the MALL does not hold them),
+    after the same warm phase.  `nbytes` is the total of bytes read and
+    written.  It is the ceiling a kernel of that size can reach on this GPU,
+    launch ramp and drain included, which the 4 GiB probes do not show."""
+    import torch
+
+    lib = _probe_library()
+    dev = torch.device("cuda:0")
+    each = nbytes // 2 if kind == "copy" else nbytes
+    each -= each % 16
+    stream = torch.cuda.current_stream().cuda_stream
+    grid = lib.gdn_hbm_probe_grid()
+    bufs = []
+    for _ in range(ROTATIONS):
+        src = torch.ones(each // 4, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src) if kind == "copy" else torch.empty(grid * 256, dtype=torch.int32,
+                                                                       device=dev)
+        bufs.append((src, dst))
+    fn = lib.gdn_hbm_probe_copy if kind == "copy" else lib.gdn_hbm_probe_read
+    calls = [(stream, src.data_ptr(), dst.data_ptr(), each, 1) for src, dst in bufs]
+    us = _time_back_to_back(fn, calls, steps)
+    moved = 2 * each if kind == "copy" else each
+    del bufs
+    return {"kind": f"{kind}_nt", "bytes": moved, "us": us, "GBps": moved / (us * 1e-6) / 1e9}
 
 
 def _c1_style_state(shape, gen, dev):
@@ -605,6 +668,41 @@ def bench_capsule(steps: int, warmup: int):
         _log(f"capsule {name}: {us:.1f} us for {states} capsules "
              f"({results[name]['capsule_GBps']:.0f} GB/s of capsule bytes)")
     assert bool((status == 0).all())
+    # SHA-256 is one serial chain per capsule, so the serialize time is the
+    # chain of the longest capsule (window position 15) whatever the number of
+    # capsules: the same serialize on an eighth of the batch (every window
+    # position still present) takes nearly as long.  The floor of one chain is
+    # its VALU instructions (905 per 64-byte block on the consumer wavefront
+    # in this build: 6 v_alignbit, 4 v_bitop3 and about 4 adds per round) at
+    # one instruction per 4 cycles at the 2.4 GHz peak engine clock.
+    small = states // 8
+    small_slot = capsule_slot(small, dev)
+    small_caps, small_offsets, small_lengths = cap.serialize(small_slot, identity)
+
+    def serialize_small():
+        return lib.capsule_serialize_launch_v1(
+            stream, *small_slot.pointers(), 1, geometry, 1, 1, small_caps.data_ptr(),
+            small_offsets.data_ptr(), small_caps.numel(), small_lengths.data_ptr(), small)
+
+    for _ in range(max(warmup, 1)):
+        assert serialize_small() == 0
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        serialize_small()
+    b.record()
+    longest = SHA_BLOCKS_PER_CAPSULE(15)
+    results["serialize_eighth_batch"] = {"capsules": small,
+                                         "us_per_batch": _events_ms([(a, b)])[0] / steps * 1e3}
+    results["longest_capsule_sha256_blocks"] = longest
+    results["chain_issue_floor_us"] = longest * 905 * 4 / 2.4e3
+    results["serialize_frac_of_chain_floor"] = (results["chain_issue_floor_us"]
+                                                / results["serialize"]["us_per_batch"])
+    _log(f"capsule serialize of {small} capsules: "
+         f"{results['serialize_eighth_batch']['us_per_batch']:.1f} us; chain floor "
+         f"{results['chain_issue_floor_us']:.1f} us")
+    del small_slot, small_caps
     results["workload"] = ("LQCAPS01 serialize / restore of B=256 x 32 heads (8192 window "
                            "states), sequence s at window position s mod 16")
     results["capsule_bytes"] = capsule_bytes
@@ -900,6 +998,7 @@ def profile_pass() -> int:
     bench_codec(2, 0)
     torch.cuda.empty_cache()
     bench_hbm_probe(repeats=2)
+    bench_valu_probe(repeats=1)
     bench_decode_projection(1, 0)
     bench_chunked_projection(1, 0)
     bench_window_step(0)
@@ -951,12 +1050,16 @@ def main() -> int:
     extra = {}
     if not args.only_codec:
         extra["hbm_probe"] = bench_hbm_probe()
+        extra["valu_probe"] = bench_valu_probe()
         dec_us, dec_sample = bench_decode_projection(args.steps, args.warmup)
         extra["decode_projection"] = {
             "workload": "config 3: B=256, 32 value heads (GQA from 16), int8 [256,32,128,128]",
             "us_per_step": dec_us, "GBps": C3_BYTES / (dec_us * 1e-6) / 1e9,
             "hbm_frac": C3_BYTES / (dec_us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
             "bytes_per_step": C3_BYTES, "rotated_state_copies": ROTATIONS}
+        probe = same_size_probe("read", C3_BYTES, args.steps)
+        probe["kernel_frac_of_probe"] = probe["us"] / dec_us
+        extra["decode_projection"]["same_size_probe"] = probe
         if not args.no_cpu:
             extra["decode_projection"]["cpu_baseline"] = cpu_baseline_projection(
                 dec_sample, False, dec_us)
@@ -970,6 +1073,9 @@ def main() -> int:
             "TFLOPs": C4_FLOPS / (chunk_us * 1e-6) / 1e12,
             "mfma_frac_of_useful_flops": C4_FLOPS / (chunk_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
             "bytes_per_step": C4_BYTES, "rotated_state_copies": ROTATIONS}
+        probe = same_size_probe("copy", C4_BYTES, args.steps)
+        probe["kernel_frac_of_probe"] = probe["us"] / chunk_us
+        extra["chunked_projection"]["same_size_probe"] = probe
         if not args.no_cpu:
             extra["chunked_projection"]["cpu_baseline"] = cpu_baseline_projection(
                 chunk_sample, True, chunk_us)

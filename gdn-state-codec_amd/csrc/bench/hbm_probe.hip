@@ -161,6 +161,56 @@ __global__ __launch_bounds__(kThreads) void contract_kernel(const uint4* __restr
   }
 }
 
+// VALU issue ceiling: every thread runs `rounds` rounds of 16 independent
+// operations (mode 0: fp32 fma, v_fma_f32; mode 1: u32 xor-add, v_xad_u32;
+// mode 2: fp64 add, v_add_f64), so each wavefront issues 16 * rounds VALU
+// instructions besides a few of loop control, with no memory traffic.
+constexpr int kValuChains = 16;
+
+template <int kMode>
+__global__ __launch_bounds__(kThreads) void valu_kernel(uint32_t* __restrict__ sink,
+                                                        uint32_t rounds, float x, float y) {
+  if constexpr (kMode == 0) {
+    float a[kValuChains];
+#pragma unroll
+    for (int i = 0; i < kValuChains; ++i) a[i] = static_cast<float>(threadIdx.x + i);
+    for (uint32_t r = 0; r < rounds; ++r) {
+#pragma unroll
+      for (int i = 0; i < kValuChains; ++i) a[i] = fmaf(a[i], x, y);
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kValuChains; ++i) total += a[i];
+    sink[blockIdx.x * kThreads + threadIdx.x] = __float_as_uint(total);
+  } else if constexpr (kMode == 1) {
+    uint32_t a[kValuChains];
+    const uint32_t step = __float_as_uint(x);
+#pragma unroll
+    for (int i = 0; i < kValuChains; ++i) a[i] = threadIdx.x + i;
+    for (uint32_t r = 0; r < rounds; ++r) {
+#pragma unroll
+      for (int i = 0; i < kValuChains; ++i) a[i] = (a[i] ^ step) + static_cast<uint32_t>(i);
+    }
+    uint32_t total = 0;
+#pragma unroll
+    for (int i = 0; i < kValuChains; ++i) total ^= a[i];
+    sink[blockIdx.x * kThreads + threadIdx.x] = total;
+  } else {
+    double a[kValuChains];
+#pragma unroll
+    for (int i = 0; i < kValuChains; ++i) a[i] = static_cast<double>(threadIdx.x + i);
+    const double step = static_cast<double>(x);
+    for (uint32_t r = 0; r < rounds; ++r) {
+#pragma unroll
+      for (int i = 0; i < kValuChains; ++i) a[i] = a[i] + step;
+    }
+    double total = 0.0;
+#pragma unroll
+    for (int i = 0; i < kValuChains; ++i) total += a[i];
+    sink[blockIdx.x * kThreads + threadIdx.x] = static_cast<uint32_t>(total);
+  }
+}
+
 }  // namespace
 
 // Grid size used by every probe: enough workgroups to fill 256 CUs many
@@ -225,5 +275,16 @@ extern "C" int32_t gdn_hbm_probe_contract(void* stream, const void* src, void* d
   hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint4*>(src),
                      static_cast<uint32_t*>(dst));
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+// VALU probe: `blocks` workgroups of 256 threads, each thread 16 * rounds
+// operations of the kind `mode` selects; sink holds blocks * 256 words.
+extern "C" int32_t gdn_valu_probe(void* stream, void* sink, uint32_t blocks, uint32_t rounds,
+                                  uint32_t mode) {
+  if (sink == nullptr || blocks == 0 || rounds == 0 || mode > 2) return 1;
+  const auto kernel = mode == 0 ? valu_kernel<0> : mode == 1 ? valu_kernel<1> : valu_kernel<2>;
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint32_t*>(sink), rounds, 1.0000001f, 0.5f);
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
