@@ -207,6 +207,146 @@ __device__ void apply_transpose(PowerShared& sh, const float* vector, float* out
   __syncthreads();
 }
 
+// The re-encode of R minus the fit, for the 128 threads of a workgroup whose
+// LDS holds the state (codes [value column][key row] at kCodeStride, the old
+// and fitted compensators ck / cv / nk / nv [dim][rank], the records rk / rc
+// [dim][record], smoothing, scales, record suffixes and the code / 127 table):
+// thread t owns key row t, whose 128 fitted cells stay in registers through
+// the smoothing, scale and code passes.  Writes the fitted residual to
+// workspace [key row][value column], next_smoothing[key], next_scales[value],
+// and hands every code of row t to sink(integral_constant column, code).  Each
+// cell is the reference's ResidualCell (window_boundary.cpp:223-251;
+// encoded_requantize.cpp:72-100 is the same expression), evaluated in its
+// order.  The column loops are unrolled at compile time (each_column) so that
+// cell[] is only ever indexed by constants and lives in VGPRs.  Uses sh.left
+// and sh.right as scratch for the column maxima.
+template <typename Sink>
+__device__ __forceinline__ void reencode_rows(PowerShared& sh, float bs, int t, float* workspace,
+                                              float* next_smoothing, float* next_scales,
+                                              Sink&& sink) {
+  const int row = t;
+  float cell[kDim];
+  {
+    // The row's operands stay as fp16 pairs (widened where used) and the
+    // window suffix products, the same for every thread, in scalar
+    // registers, leaving the vector registers to the cells.
+    const float s = sh.smoothing[row];
+    uint32_t ck2[kRank / 2], nk2[kRank / 2], rk2[kWindow / 2];
+    float suffix[kWindow];
+#pragma unroll
+    for (int i = 0; i < kRank / 2; ++i) {
+      ck2[i] = reinterpret_cast<const uint32_t*>(sh.ck + row * kRank)[i];
+      nk2[i] = reinterpret_cast<const uint32_t*>(sh.nk + row * kRank)[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kWindow / 2; ++i) rk2[i] = reinterpret_cast<const uint32_t*>(sh.rk + row * kWindow)[i];
+#pragma unroll
+    for (int j = 0; j < kWindow; ++j) {
+      suffix[j] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sh.record_suffix[j])));
+    }
+    const auto low = [](uint32_t pair, int i) { return h2f(i & 1 ? pair >> 16 : pair & 0xFFFFu); };
+    each_column([&](auto c) {
+      constexpr int column = decltype(c)::value;
+      // Opaque to the compiler, so the pairs are widened per column instead of
+      // once into 24 long-lived registers.
+#pragma unroll
+      for (int i = 0; i < kRank / 2; ++i) asm volatile("" : "+v"(ck2[i]), "+v"(nk2[i]));
+#pragma unroll
+      for (int i = 0; i < kWindow / 2; ++i) asm volatile("" : "+v"(rk2[i]));
+      float value = code_value(sh, sh.code[column * kCodeStride + row]) * s *
+                    sh.scales[column] * bs;
+#pragma unroll
+      for (int r = 0; r < kRank; ++r) {
+        value += low(ck2[r / 2], r) * h2f(sh.cv[column * kRank + r]) * bs;
+        value -= low(nk2[r / 2], r) * h2f(sh.nv[column * kRank + r]);
+      }
+      const uint4* const rc4 = reinterpret_cast<const uint4*>(sh.rc + column * kWindow);
+      const uint4 c0 = rc4[0], c1 = rc4[1];
+      const uint32_t rc2[kWindow / 2] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+      for (int j = 0; j < kWindow; ++j) {
+        value += low(rk2[j / 2], j) * low(rc2[j / 2], j) * suffix[j];
+      }
+      cell[column] = value;
+      // One column's operands at a time: the scheduler would otherwise hoist
+      // the LDS reads of many columns ahead of their use.
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+  {
+    float4* const work = reinterpret_cast<float4*>(workspace + row * kDim);
+#pragma unroll
+    for (int q = 0; q < kDim / 4; ++q) {
+      work[q] = make_float4(cell[4 * q], cell[4 * q + 1], cell[4 * q + 2], cell[4 * q + 3]);
+    }
+  }
+
+  // ---- fresh smoothing (row t): sequential sum of |cell| over the columns ----
+  float s_new;
+  {
+    float mean_absolute = 0.0f;
+    each_column([&](auto c) { mean_absolute += fabsf(cell[decltype(c)::value]); });
+    const float mean = mean_absolute / 128.0f;
+    s_new = newton_sqrt(mean > kBoundaryFloor ? mean : kBoundaryFloor);
+    next_smoothing[row] = s_new;
+  }
+  // m = cell / s_new is formed where it is used (the scale and code passes
+  // each divide again, to the same bits) rather than stored over the cells.
+
+  // ---- scales: max over rows of |cell / s| per column -------------------------
+  // The reference keeps `value > maximum ? value : maximum` from 0 over the
+  // rows, which skips NaNs; fmaxf(|m|, 0) maps a NaN to 0 and leaves every
+  // other |m| alone, and a maximum of those is exact in any order.  Each
+  // wavefront reduces its 64 rows with quarter-width reduce-scatters (32
+  // columns across 64 lanes: lane L ends with column L % 32), then the two
+  // wavefronts' maxima meet in LDS.
+  const int lane = t & 63;
+  const int wave = t >> 6;
+#pragma unroll
+  for (int quarter = 0; quarter < 4; ++quarter) {
+    const auto magnitude = [&](int i) {
+      return fmaxf(fabsf(cell[32 * quarter + i] / s_new), 0.0f);
+    };
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float lo = fold_max<16>(magnitude(i), magnitude(16 + i), lane);
+      const float hi = fold_max<16>(magnitude(8 + i), magnitude(24 + i), lane);
+      v[i] = fold_max<8>(lo, hi, lane);
+      if (i % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = fold_max<4>(v[i], v[i + 4], lane);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) v[i] = fold_max<2>(v[i], v[i + 2], lane);
+    v[0] = fold_max<1>(v[0], v[1], lane);
+    v[0] = max_partner<32>(v[0]);
+    if (lane < 32) {
+      (wave == 0 ? sh.left : sh.right)[32 * quarter + lane] = v[0];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __syncthreads();  // both wavefronts' column maxima; every cell has been evaluated
+  {
+    const float maximum = fmaxf(sh.left[t], sh.right[t]);
+    next_scales[t] = maximum;
+    sh.left[t] = maximum;  // thread t's own slot: no other thread reads it yet
+  }
+  __syncthreads();
+
+  // ---- codes: round-half-away (:336-345), handed to the caller's sink ------
+  each_column([&](auto c) {
+    constexpr int column = decltype(c)::value;
+    const float maximum = sh.left[column];
+    float q = maximum == 0.0f ? 0.0f : cell[column] / s_new / maximum * 127.0f;
+    q += q >= 0.0f ? 0.5f : -0.5f;
+    q = q > 127.0f ? 127.0f : q;
+    q = q < -127.0f ? -127.0f : q;
+    sink(c, static_cast<int8_t>(static_cast<int>(q)));
+    if constexpr (column % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+  });
+}
+
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void power_refit_kernel(PowerArgs a) {
   extern __shared__ __align__(16) unsigned char dynamic[];
   PowerShared& sh = *reinterpret_cast<PowerShared*>(dynamic);
@@ -274,134 +414,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     __syncthreads();
   }
 
-  // ---- R minus the fit: row t in registers, and into the workspace ----------
-  // Thread t owns key row t: its 128 fitted cells stay in registers through
-  // the smoothing, scale and code passes, so the workspace is written once
-  // and never read back.  Each cell is the reference's ResidualCell
-  // (:223-251), evaluated in its order.  The column loops are unrolled at
-  // compile time (each_column) so that cell[] is only ever indexed by
-  // constants and lives in VGPRs.
-  const int row = t;
-  float cell[kDim];
-  {
-    // The row's operands stay as fp16 pairs (widened where used) and the
-    // window suffix products, the same for every thread, in scalar
-    // registers, leaving the vector registers to the cells.
-    const float s = sh.smoothing[row];
-    uint32_t ck2[kRank / 2], nk2[kRank / 2], rk2[kWindow / 2];
-    float suffix[kWindow];
-#pragma unroll
-    for (int i = 0; i < kRank / 2; ++i) {
-      ck2[i] = reinterpret_cast<const uint32_t*>(sh.ck + row * kRank)[i];
-      nk2[i] = reinterpret_cast<const uint32_t*>(sh.nk + row * kRank)[i];
-    }
-#pragma unroll
-    for (int i = 0; i < kWindow / 2; ++i) rk2[i] = reinterpret_cast<const uint32_t*>(sh.rk + row * kWindow)[i];
-#pragma unroll
-    for (int j = 0; j < kWindow; ++j) {
-      suffix[j] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sh.record_suffix[j])));
-    }
-    const auto low = [](uint32_t pair, int i) { return h2f(i & 1 ? pair >> 16 : pair & 0xFFFFu); };
-    each_column([&](auto c) {
-      constexpr int column = decltype(c)::value;
-      // Opaque to the compiler, so the pairs are widened per column instead of
-      // once into 24 long-lived registers.
-#pragma unroll
-      for (int i = 0; i < kRank / 2; ++i) asm volatile("" : "+v"(ck2[i]), "+v"(nk2[i]));
-#pragma unroll
-      for (int i = 0; i < kWindow / 2; ++i) asm volatile("" : "+v"(rk2[i]));
-      float value = code_value(sh, sh.code[column * kCodeStride + row]) * s *
-                    sh.scales[column] * bs;
-#pragma unroll
-      for (int r = 0; r < kRank; ++r) {
-        value += low(ck2[r / 2], r) * h2f(sh.cv[column * kRank + r]) * bs;
-        value -= low(nk2[r / 2], r) * h2f(sh.nv[column * kRank + r]);
-      }
-      const uint4* const rc4 = reinterpret_cast<const uint4*>(sh.rc + column * kWindow);
-      const uint4 c0 = rc4[0], c1 = rc4[1];
-      const uint32_t rc2[kWindow / 2] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-#pragma unroll
-      for (int j = 0; j < kWindow; ++j) {
-        value += low(rk2[j / 2], j) * low(rc2[j / 2], j) * suffix[j];
-      }
-      cell[column] = value;
-      // One column's operands at a time: the scheduler would otherwise hoist
-      // the LDS reads of many columns ahead of their use.
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  }
-  {
-    float4* const work = reinterpret_cast<float4*>((a.workspace + state * kTile) + row * kDim);
-#pragma unroll
-    for (int q = 0; q < kDim / 4; ++q) {
-      work[q] = make_float4(cell[4 * q], cell[4 * q + 1], cell[4 * q + 2], cell[4 * q + 3]);
-    }
-  }
-
-  // ---- fresh smoothing (row t): sequential sum of |cell| over the columns ----
-  float s_new;
-  {
-    float mean_absolute = 0.0f;
-    each_column([&](auto c) { mean_absolute += fabsf(cell[decltype(c)::value]); });
-    const float mean = mean_absolute / 128.0f;
-    s_new = newton_sqrt(mean > kBoundaryFloor ? mean : kBoundaryFloor);
-    (a.next_smoothing + vb)[row] = s_new;
-  }
-  // m = cell / s_new is formed where it is used (the scale and code passes
-  // each divide again, to the same bits) rather than stored over the cells.
-
-  // ---- scales: max over rows of |cell / s| per column -------------------------
-  // The reference keeps `value > maximum ? value : maximum` from 0 over the
-  // rows, which skips NaNs; fmaxf(|m|, 0) maps a NaN to 0 and leaves every
-  // other |m| alone, and a maximum of those is exact in any order.  Each
-  // wavefront reduces its 64 rows with quarter-width reduce-scatters (32
-  // columns across 64 lanes: lane L ends with column L % 32), then the two
-  // wavefronts' maxima meet in LDS.
-  const int lane = t & 63;
-  const int wave = t >> 6;
-#pragma unroll
-  for (int quarter = 0; quarter < 4; ++quarter) {
-    const auto magnitude = [&](int i) {
-      return fmaxf(fabsf(cell[32 * quarter + i] / s_new), 0.0f);
-    };
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float lo = fold_max<16>(magnitude(i), magnitude(16 + i), lane);
-      const float hi = fold_max<16>(magnitude(8 + i), magnitude(24 + i), lane);
-      v[i] = fold_max<8>(lo, hi, lane);
-      if (i % 2 == 1) __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = fold_max<4>(v[i], v[i + 4], lane);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) v[i] = fold_max<2>(v[i], v[i + 2], lane);
-    v[0] = fold_max<1>(v[0], v[1], lane);
-    v[0] = max_partner<32>(v[0]);
-    if (lane < 32) {
-      (wave == 0 ? sh.left : sh.right)[32 * quarter + lane] = v[0];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  __syncthreads();  // both wavefronts' column maxima; every cell has been evaluated
-  {
-    const float maximum = fmaxf(sh.left[t], sh.right[t]);
-    (a.next_scales + vb)[t] = maximum;
-    sh.left[t] = maximum;  // thread t's own slot: no other thread reads it yet
-  }
-  __syncthreads();
-
-  // ---- codes: round-half-away (:336-345), staged in the code area ------------
-  each_column([&](auto c) {
-    constexpr int column = decltype(c)::value;
-    const float maximum = sh.left[column];
-    float q = maximum == 0.0f ? 0.0f : cell[column] / s_new / maximum * 127.0f;
-    q += q >= 0.0f ? 0.5f : -0.5f;
-    q = q > 127.0f ? 127.0f : q;
-    q = q < -127.0f ? -127.0f : q;
-    sh.code[column * kCodeStride + row] = static_cast<int8_t>(static_cast<int>(q));
-    if constexpr (column % 4 == 3) __builtin_amdgcn_sched_barrier(0);
-  });
+  // ---- R minus the fit, re-encoded; codes staged in the code area ------------
+  // The workspace is written once and never read back.
+  reencode_rows(sh, bs, t, a.workspace + state * kTile, a.next_smoothing + vb, a.next_scales + vb,
+                [&](auto c, int8_t code) {
+                  sh.code[decltype(c)::value * kCodeStride + t] = code;
+                });
   __syncthreads();
   // next_residual [value column][key row]: each round of 16 columns, eight
   // lanes write one whole 128-byte column.
@@ -426,6 +444,96 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   if (t < kWindow) a.record_decay[rb + t] = 0.0f;
   __syncthreads();  // every thread has read the position word above
   if (t == 0) a.positions[state * kPositionStride] = 0u;
+}
+
+// ---- encoded_requantize -----------------------------------------------------
+
+struct RequantizeArgs {
+  const int8_t* residual;  // [state][row = smoothing axis][column = scale axis]
+  const float* smoothing;
+  const float* scales;
+  const uint16_t* old_left;  // [state][dim][rank]
+  const uint16_t* old_right;
+  const float* record_decay;
+  const uint16_t* record_left;  // [state][record][dim]
+  const uint16_t* record_right;
+  const uint16_t* new_left;  // [state][rank][dim]
+  const uint16_t* new_right;
+  int8_t* next_residual;  // [state][row][column]
+  float* next_smoothing;
+  float* next_scales;
+  uint16_t* next_left;  // [state][dim][rank]
+  uint16_t* next_right;
+  float* workspace;  // [state][row][column]
+};
+
+// EncodedRequantize::Process (encoded_requantize.cpp:102-166): the window
+// operator minus the committed ranks re-encoded.  The state is staged in the
+// power refit's LDS layout (codes transposed to [column][row], the [rank][dim]
+// bases to [dim][rank], the records to [dim][record]) and re-encoded by the
+// same reencode_rows; thread t packs the codes of its row in registers and
+// stores the row as eight 16-byte words.
+__global__ __launch_bounds__(kThreads) void encoded_requantize_kernel(RequantizeArgs a) {
+  extern __shared__ __align__(16) unsigned char dynamic[];
+  PowerShared& sh = *reinterpret_cast<PowerShared*>(dynamic);
+  const int t = threadIdx.x;
+  const uint64_t state = blockIdx.x;
+  const uint64_t vb = state * kDim;
+  const uint64_t rb = state * kWindow;
+
+  const uint32_t* words = reinterpret_cast<const uint32_t*>(a.residual + state * kTile);
+  for (int i = t; i < kTile / 4; i += kThreads) {
+    const uint32_t w = words[i];
+    const int row = (4 * i) / kDim, column = (4 * i) % kDim;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      sh.code[(column + b) * kCodeStride + row] = static_cast<int8_t>(w >> (8 * b));
+    }
+  }
+  for (int i = t; i < kDim * kRank; i += kThreads) {
+    const int dimension = i / kRank, rank = i % kRank;
+    sh.ck[i] = a.old_left[vb * kRank + i];
+    sh.cv[i] = a.old_right[vb * kRank + i];
+    sh.nk[i] = a.new_left[(state * kRank + rank) * kDim + dimension];
+    sh.nv[i] = a.new_right[(state * kRank + rank) * kDim + dimension];
+  }
+  for (int i = t; i < kWindow * kDim; i += kThreads) {
+    const int j = i / kDim, dimension = i % kDim;
+    sh.rk[dimension * kWindow + j] = a.record_left[rb * kDim + i];
+    sh.rc[dimension * kWindow + j] = a.record_right[rb * kDim + i];
+  }
+  sh.smoothing[t] = (a.smoothing + vb)[t];
+  sh.scales[t] = (a.scales + vb)[t];
+  sh.code_value[t] = code_over_127(static_cast<int8_t>(t));
+  sh.code_value[t + kThreads] = code_over_127(static_cast<int8_t>(t + kThreads));
+  // The suffix products (:106-111), computed identically by every thread.
+  float bs = 1.0f;
+  for (int j = kWindow - 1; j >= 0; --j) {
+    if (t == 0) sh.record_suffix[j] = bs;
+    bs *= a.record_decay[rb + j];
+  }
+  bs = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bs)));
+  __syncthreads();
+
+  uint32_t packed[kDim / 4];
+#pragma unroll
+  for (int q = 0; q < kDim / 4; ++q) packed[q] = 0u;
+  reencode_rows(sh, bs, t, a.workspace + state * kTile, a.next_smoothing + vb, a.next_scales + vb,
+                [&](auto c, int8_t code) {
+                  constexpr int column = decltype(c)::value;
+                  packed[column / 4] |= static_cast<uint32_t>(static_cast<uint8_t>(code))
+                                        << (8 * (column % 4));
+                });
+  uint4* const out = reinterpret_cast<uint4*>(a.next_residual + state * kTile + t * kDim);
+#pragma unroll
+  for (int q = 0; q < kDim / 16; ++q) {
+    out[q] = make_uint4(packed[4 * q], packed[4 * q + 1], packed[4 * q + 2], packed[4 * q + 3]);
+  }
+  // The committed bases in the [dim][rank] layout: the LDS copies already are.
+  for (int i = t; i < kDim * kRank; i += kThreads) {
+    a.next_left[vb * kRank + i] = sh.nk[i];
+    a.next_right[vb * kRank + i] = sh.nv[i];
+  }
 }
 
 // The residual workspace of the allocation-free refit entry point: room for
@@ -530,4 +638,33 @@ extern "C" int32_t statecentric_gdn_state_codec_window_boundary_noalloc_launch_v
                                  record_corrections, positions, next_residual, next_smoothing,
                                  next_scales, next_compensator_keys, next_compensator_values,
                                  workspace, states, power_iterations);
+}
+
+// encoded_requantize_launch_v1 (encoded_requantize.cpp:102-166, admission
+// :189-215): every state re-encoded; see the kernel above.
+extern "C" int32_t statecentric_gdn_state_codec_encoded_requantize_launch_v1(
+    void* stream, const int8_t* residual, const float* smoothing, const float* scales,
+    const uint16_t* old_left, const uint16_t* old_right, const float* record_decay,
+    const uint16_t* record_left, const uint16_t* record_right, const uint16_t* new_left,
+    const uint16_t* new_right, int8_t* next_residual, float* next_smoothing,
+    float* next_scales, uint16_t* next_left, uint16_t* next_right,
+    float* residual_workspace, uint32_t states) {
+  if (!residual || !smoothing || !scales || !old_left || !old_right || !record_decay ||
+      !record_left || !record_right || !new_left || !new_right || !next_residual ||
+      !next_smoothing || !next_scales || !next_left || !next_right || !residual_workspace ||
+      states == 0 || states > gdn::kMaxWindowStates ||
+      !gdn::aligned16(residual, smoothing, scales, old_left, old_right, record_decay,
+                      record_left, record_right, new_left, new_right, next_residual,
+                      next_smoothing, next_scales, next_left, next_right, residual_workspace)) {
+    return gdn::kStatusInvalidArgument;
+  }
+  const gdn::RequantizeArgs args{residual, smoothing, scales, old_left, old_right,
+                                 record_decay, record_left, record_right, new_left, new_right,
+                                 next_residual, next_smoothing, next_scales, next_left,
+                                 next_right, residual_workspace};
+  void* pointers[] = {const_cast<gdn::RequantizeArgs*>(&args)};
+  const hipError_t status = hipLaunchKernel(
+      reinterpret_cast<const void*>(gdn::encoded_requantize_kernel), dim3(states),
+      dim3(gdn::kThreads), pointers, sizeof(gdn::PowerShared), static_cast<hipStream_t>(stream));
+  return status == hipSuccess ? gdn::kStatusOk : gdn::kStatusLaunchFailed;
 }

@@ -152,6 +152,59 @@ int32_t statecentric_gdn_state_codec_int8_cube_matmul_launch_v1(
     void* stream, const int8_t* a, const int8_t* b, int32_t* c, uint32_t states,
     uint32_t transpose_a, void* workspace, void* tiling, uint32_t blocks);
 
+/* ---- the reference's device rank-4 chain over an encoded boundary ----------
+ * (driven by host/gdn_state_codec_encoded_projection_probe.cpp:571-677:
+ * prepare_int8_vector -> int8_cube_matmul -> finish_encoded_projection, forward
+ * and transposed, per power iteration; then prepare -> GEMM ->
+ * commit_encoded_rank per rank; then encoded_requantize.)  Per state: vector
+ * operands fp16 / int32 / fp32 [128][16] of which column 0 is the vector;
+ * dynamic_scale fp32 [8] (element 0); old_left / old_right fp16 [128][4]
+ * ([dim][rank]); new_left / new_right fp16 [4][128] ([rank][dim]); record_left /
+ * record_right fp16 [16][128]; record_decay fp32 [16]; smoothing / scales fp32
+ * [128].  Each row of the window operator (transpose 0, rows on the smoothing
+ * axis) or of its transpose is p * dyn / 127 * axis * B + the old ranks * B -
+ * the first `fitted_ranks` fitted ranks + the records * their suffixes, with
+ * every sum sequential in the reference's order: results are bit-identical to
+ * the reference's scalar code restated on the CPU.  1 <= states <= 16384. */
+
+/* output column 0 = fp16(value / |value|) (0 when |value|^2 <= 1e-20), columns
+ * 1..15 = 0; fitted_ranks <= 4, transpose <= 1.  Replaces
+ * windowed_gdn_kernel.h:151-160 (kernel/gdn_state_codec_encoded_projection.cpp:778-820,
+ * 964-990). */
+int32_t statecentric_gdn_state_codec_finish_encoded_projection_launch_v1(
+    void* stream, const int32_t* projected, const float* dynamic_scale,
+    const uint16_t* input, const float* smoothing, const float* scales,
+    const uint16_t* old_left, const uint16_t* old_right, const float* record_decay,
+    const uint16_t* record_left, const uint16_t* record_right, const uint16_t* new_left,
+    const uint16_t* new_right, uint16_t* output, uint32_t states, uint32_t fitted_ranks,
+    uint32_t transpose);
+
+/* The forward rows with ranks 0..rank-1 deflated: corrected column 0 = value
+ * (other columns untouched), new_left[rank] = fp16(value), new_right[rank] =
+ * the input's fp16 bits; rank < 4.  Replaces windowed_gdn_kernel.h:162-169
+ * (encoded_projection.cpp:822-865, 992-1015). */
+int32_t statecentric_gdn_state_codec_commit_encoded_rank_launch_v1(
+    void* stream, const int32_t* projected, const float* dynamic_scale,
+    const uint16_t* input, const float* smoothing, const float* scales,
+    const uint16_t* old_left, const uint16_t* old_right, const float* record_decay,
+    const uint16_t* record_left, const uint16_t* record_right, uint16_t* new_left,
+    uint16_t* new_right, float* corrected, uint32_t states, uint32_t rank);
+
+/* residual int8 [S][128][128] as [smoothing axis][scale axis]; the window
+ * operator minus new_left^T new_right, re-encoded exactly as the rank-4
+ * window-boundary refit re-encodes (fresh smoothing, absmax scales,
+ * round-half-away codes, the fitted residual into residual_workspace
+ * [S][128][128]); next_left / next_right = the new bases as [dim][rank].
+ * next_* must not alias the inputs.  Replaces windowed_gdn_kernel.h:171-179
+ * (kernel/gdn_state_codec_encoded_requantize.cpp:102-166, 189-215). */
+int32_t statecentric_gdn_state_codec_encoded_requantize_launch_v1(
+    void* stream, const int8_t* residual, const float* smoothing, const float* scales,
+    const uint16_t* old_left, const uint16_t* old_right, const float* record_decay,
+    const uint16_t* record_left, const uint16_t* record_right, const uint16_t* new_left,
+    const uint16_t* new_right, int8_t* next_residual, float* next_smoothing,
+    float* next_scales, uint16_t* next_left, uint16_t* next_right,
+    float* residual_workspace, uint32_t states);
+
 /* ---- decode runtime (host/gdn_state_codec_decode_runtime.cpp:72-148) ------
  * create returns a process-wide handle for `states` (1..16384; nullptr when a
  * live handle has a different count), reference-counted; destroy drops one

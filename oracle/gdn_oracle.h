@@ -320,6 +320,33 @@ void gdn_oracle_window_boundary_power(
     uint16_t* next_comp_keys, uint16_t* next_comp_values,
     float* residual_workspace, uint32_t states, uint32_t power_iterations);
 
+/* ---- device rank-4 chain over an encoded boundary (gdn_encoded_oracle.c) ---
+ *
+ * encoded_projection.cpp:82-163, 778-865 and encoded_requantize.cpp:72-166;
+ * layouts in the header of gdn_encoded_oracle.c.  Parity pins: the requantize
+ * against the pinned power-refit restatement fed the same fit, float64 brute
+ * force of the operator rows, closed forms of the commit outputs, and planted
+ * negative controls (tests/test_oracle_encoded.py). */
+void gdn_oracle_finish_encoded_projection(
+    const int32_t* projected, const float* dynamic_scale, const uint16_t* input,
+    const float* smoothing, const float* scales, const uint16_t* old_left,
+    const uint16_t* old_right, const float* record_decay, const uint16_t* record_left,
+    const uint16_t* record_right, const uint16_t* new_left, const uint16_t* new_right,
+    uint16_t* output, uint32_t states, uint32_t fitted_ranks, uint32_t transpose);
+void gdn_oracle_commit_encoded_rank(
+    const int32_t* projected, const float* dynamic_scale, const uint16_t* input,
+    const float* smoothing, const float* scales, const uint16_t* old_left,
+    const uint16_t* old_right, const float* record_decay, const uint16_t* record_left,
+    const uint16_t* record_right, uint16_t* new_left, uint16_t* new_right,
+    float* corrected, uint32_t states, uint32_t rank);
+void gdn_oracle_encoded_requantize(
+    const int8_t* residual, const float* smoothing, const float* scales,
+    const uint16_t* old_left, const uint16_t* old_right, const float* record_decay,
+    const uint16_t* record_left, const uint16_t* record_right, const uint16_t* new_left,
+    const uint16_t* new_right, int8_t* next_residual, float* next_smoothing,
+    float* next_scales, uint16_t* next_left, uint16_t* next_right,
+    float* residual_workspace, uint32_t states);
+
 /* ---- capsule wire format LQCAPS01 (gdn_capsule_oracle.c) ------------------
  *
  * Parity pins: SHA-256 vs FIPS 180-4 vectors, hashlib and the reference's

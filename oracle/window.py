@@ -356,3 +356,65 @@ def window_boundary_power(buf: dict, out: dict, workspace, power_iterations: int
         _ptr(buf["positions"]), _ptr(out["next_residual"]), _ptr(out["next_smoothing"]),
         _ptr(out["next_scales"]), _ptr(out["next_compensator_keys"]),
         _ptr(out["next_compensator_values"]), _ptr(workspace), states, power_iterations)
+
+
+# ------------------------------------------- device rank-4 chain (encoded boundary)
+
+def _bind_encoded(l):
+    if getattr(l, "_encoded_bound", False):
+        return l
+    for name in ("gdn_oracle_finish_encoded_projection",):
+        getattr(l, name).argtypes = [_P] * 13 + [_U32] * 3
+        getattr(l, name).restype = None
+    l.gdn_oracle_commit_encoded_rank.argtypes = [_P] * 13 + [_U32] * 2
+    l.gdn_oracle_commit_encoded_rank.restype = None
+    l.gdn_oracle_encoded_requantize.argtypes = [_P] * 16 + [_U32]
+    l.gdn_oracle_encoded_requantize.restype = None
+    l._encoded_bound = True
+    return l
+
+
+ENCODED_OPERANDS = ("smoothing", "scales", "old_left", "old_right", "record_decay",
+                    "record_left", "record_right")
+
+
+def finish_encoded_projection(enc: dict, projected, dynamic_scale, inputs, fitted_ranks: int,
+                              transpose: int):
+    """finish_encoded_projection_launch_v1 -> fp16 bits [S][128][16].  ``enc``
+    holds the operands named in ENCODED_OPERANDS plus new_left / new_right."""
+    states = enc["smoothing"].shape[0]
+    output = np.zeros((states, DIM, 16), np.uint16)
+    _bind_encoded(_l()).gdn_oracle_finish_encoded_projection(
+        _ptr(_c(projected, np.int32)), _ptr(_c(dynamic_scale, np.float32)),
+        _ptr(_c(inputs, np.uint16)), *(_ptr(enc[k]) for k in ENCODED_OPERANDS),
+        _ptr(enc["new_left"]), _ptr(enc["new_right"]), _ptr(output), states, fitted_ranks,
+        transpose)
+    return output
+
+
+def commit_encoded_rank(enc: dict, projected, dynamic_scale, inputs, corrected, rank: int):
+    """commit_encoded_rank_launch_v1; updates enc['new_left'], enc['new_right']
+    (rank ``rank``) and column 0 of ``corrected`` in place."""
+    states = enc["smoothing"].shape[0]
+    _bind_encoded(_l()).gdn_oracle_commit_encoded_rank(
+        _ptr(_c(projected, np.int32)), _ptr(_c(dynamic_scale, np.float32)),
+        _ptr(_c(inputs, np.uint16)), *(_ptr(enc[k]) for k in ENCODED_OPERANDS),
+        _ptr(enc["new_left"]), _ptr(enc["new_right"]), _ptr(corrected), states, rank)
+
+
+def encoded_requantize(enc: dict, residual):
+    """encoded_requantize_launch_v1 -> dict of next_residual, next_smoothing,
+    next_scales, next_left, next_right, workspace."""
+    states = enc["smoothing"].shape[0]
+    out = {"next_residual": np.zeros((states, DIM, DIM), np.int8),
+           "next_smoothing": np.zeros((states, DIM), np.float32),
+           "next_scales": np.zeros((states, DIM), np.float32),
+           "next_left": np.zeros((states, DIM, RANK), np.uint16),
+           "next_right": np.zeros((states, DIM, RANK), np.uint16),
+           "workspace": np.zeros((states, DIM, DIM), np.float32)}
+    _bind_encoded(_l()).gdn_oracle_encoded_requantize(
+        _ptr(_c(residual, np.int8)), *(_ptr(enc[k]) for k in ENCODED_OPERANDS),
+        _ptr(enc["new_left"]), _ptr(enc["new_right"]), _ptr(out["next_residual"]),
+        _ptr(out["next_smoothing"]), _ptr(out["next_scales"]), _ptr(out["next_left"]),
+        _ptr(out["next_right"]), _ptr(out["workspace"]), states)
+    return out

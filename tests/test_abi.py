@@ -170,6 +170,30 @@ def test_boundary_entry_points_admit_like_the_reference(lib):
     assert lib.bf16_cube_matmul_launch_v1(None, p, p, p, 130, p, p, 65) == 1
 
 
+def test_encoded_rank_chain_admits_like_the_reference(lib):
+    """encoded_projection.cpp:972-976, 1000-1004; encoded_requantize.cpp:200-204:
+    every pointer required, 1 <= states <= 16384, fitted_ranks <= 4,
+    transpose <= 1, rank < 4; all rejected before any HIP call."""
+    p = ctypes.c_void_p(16)
+    thirteen = [p] * 13
+    for states, fitted, transpose in ((0, 0, 0), (16385, 0, 0), (8, 5, 0), (8, 0, 2)):
+        assert lib.finish_encoded_projection_launch_v1(
+            None, *thirteen, states, fitted, transpose) == 1
+    for states, rank in ((0, 0), (16385, 0), (8, 4)):
+        assert lib.commit_encoded_rank_launch_v1(None, *thirteen, states, rank) == 1
+    for states in (0, 16385):
+        assert lib.encoded_requantize_launch_v1(None, *([p] * 16), states) == 1
+    for i in range(13):
+        args = list(thirteen)
+        args[i] = None
+        assert lib.finish_encoded_projection_launch_v1(None, *args, 8, 4, 1) == 1
+        assert lib.commit_encoded_rank_launch_v1(None, *args, 8, 3) == 1
+    for i in range(16):
+        args = [p] * 16
+        args[i] = None
+        assert lib.encoded_requantize_launch_v1(None, *args, 8) == 1
+
+
 def test_noalloc_refit_admission(lib):
     """The allocation-free refit: every pointer required, at most 512 states
     when the power refit needs the scratch workspace, 16384 without it, and
@@ -266,6 +290,9 @@ _ALIGNMENT_CASES = {
     "finish_decode_pair_launch_v1": [None] + ["P"] * 15 + [2],
     "finish_decode_pair_bf16_launch_v1": [None] + ["P"] * 15 + [2],
     "window_boundary_launch_v1": [None] + ["P"] * 15 + [2, 0],
+    "finish_encoded_projection_launch_v1": [None] + ["P"] * 13 + [2, 4, 1],
+    "commit_encoded_rank_launch_v1": [None] + ["P"] * 13 + [2, 3],
+    "encoded_requantize_launch_v1": [None] + ["P"] * 16 + [2],
     "window_boundary_noalloc_launch_v1": [None] + ["P"] * 14 + [2, 4],
     "boundary_scale_records_launch_v1": [None] + ["P"] * 3 + [2],
     "window_boundary_cube_finish_launch_v1": [None] + ["P"] * 15 + [2],
