@@ -591,6 +591,97 @@ def bench_refit(steps: int, warmup: int):
     return results
 
 
+def encoded_rank_bytes() -> dict:
+    """Algorithmic HBM bytes per state of the device rank-4 chain's finishing
+    kernels: finish / commit read column 0 of the int32 projection and the fp16
+    input (128 values each), the output-axis scales, the dynamic scale, both
+    old and both fitted fp16 bases ([128][4] and [4][128], 1 KiB each), both
+    fp16 record sides (4 KiB each) and the 16 gates; finish writes the fp16
+    [128][16] output, commit column 0 of the fp32 corrected vector and one rank
+    of each fitted basis.  encoded_requantize reads the int8 boundary, smoothing,
+    scales, the four bases, the gates and records, and writes the codes,
+    smoothing, scales, the transposed bases and the fp32 workspace."""
+    operands = 128 * 4 + 128 * 2 + 128 * 4 + 4 + 4 * 1024 + 2 * 4096 + 16 * 4
+    return {"finish": operands + 128 * 16 * 2,
+            "commit": operands + 128 * 4 + 2 * 128 * 2,
+            "requantize": (128 * 128 + 2 * 128 * 4 + 4 * 1024 + 16 * 4 + 2 * 4096)
+                          + (128 * 128 + 2 * 128 * 4 + 2 * 1024 + 128 * 128 * 4)}
+
+
+def bench_encoded_rank(steps: int):
+    """The finishing kernels of the reference's device rank-4 chain over an
+    encoded boundary at 8192 states (B=256 x 32 heads): finish_encoded_projection
+    (4 fitted ranks), commit_encoded_rank (rank 3) and encoded_requantize, each
+    timed back to back over rotated operand copies after a warm phase."""
+    import torch
+
+    from gdn_state_codec import native
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(17)
+    states = WINDOW_STATES
+
+    def f16(*shape, scale=0.05):
+        return (torch.randn(shape, generator=gen, device=dev) * scale).to(torch.float16)
+
+    sets = []
+    for _ in range(ROTATIONS):
+        op = {"projected": torch.randint(-200000, 200000, (states, 128, 16), generator=gen,
+                                         device=dev, dtype=torch.int32),
+              "dyn": torch.full((states, 8), 1e-3, device=dev),
+              "input": f16(states, 128, 16, scale=0.1),
+              "smoothing": torch.rand((states, 128), generator=gen, device=dev) + 0.5,
+              "scales": torch.rand((states, 128), generator=gen, device=dev) + 0.5,
+              "old_left": f16(states, 128, 4), "old_right": f16(states, 128, 4),
+              "decay": torch.rand((states, 16), generator=gen, device=dev) * 0.06 + 0.93,
+              "record_left": f16(states, 16, 128), "record_right": f16(states, 16, 128),
+              "new_left": f16(states, 4, 128), "new_right": f16(states, 4, 128),
+              "residual": torch.randint(-127, 128, (states, 128, 128), generator=gen,
+                                        device=dev, dtype=torch.int8),
+              "output": torch.empty((states, 128, 16), dtype=torch.float16, device=dev),
+              "corrected": torch.empty((states, 128, 16), device=dev)}
+        sets.append(op)
+    nxt = {"residual": torch.empty((states, 128, 128), dtype=torch.int8, device=dev),
+           "smoothing": torch.empty((states, 128), device=dev),
+           "scales": torch.empty((states, 128), device=dev),
+           "left": torch.empty((states, 128, 4), dtype=torch.float16, device=dev),
+           "right": torch.empty((states, 128, 4), dtype=torch.float16, device=dev),
+           "workspace": torch.empty((states, 128, 128), device=dev)}
+    lib, stream = native(), torch.cuda.current_stream().cuda_stream
+
+    def operands(op):
+        return [op[k].data_ptr() for k in ("smoothing", "scales", "old_left", "old_right",
+                                           "decay", "record_left", "record_right")]
+
+    finish = [(stream, op["projected"].data_ptr(), op["dyn"].data_ptr(), op["input"].data_ptr(),
+               *operands(op), op["new_left"].data_ptr(), op["new_right"].data_ptr(),
+               op["output"].data_ptr(), states, 4, 0) for op in sets]
+    commit = [(stream, op["projected"].data_ptr(), op["dyn"].data_ptr(), op["input"].data_ptr(),
+               *operands(op), op["new_left"].data_ptr(), op["new_right"].data_ptr(),
+               op["corrected"].data_ptr(), states, 3) for op in sets]
+    requantize = [(stream, op["residual"].data_ptr(), *operands(op), op["new_left"].data_ptr(),
+                   op["new_right"].data_ptr(), *(nxt[k].data_ptr() for k in nxt), states)
+                  for op in sets]
+    per_state = encoded_rank_bytes()
+    results = {}
+    for name, fn, calls in (
+            ("finish", lib.finish_encoded_projection_launch_v1, finish),
+            ("commit", lib.commit_encoded_rank_launch_v1, commit),
+            ("requantize", lib.encoded_requantize_launch_v1, requantize)):
+        us = _time_back_to_back(fn, calls, steps)
+        nbytes = per_state[name] * states
+        results[name] = {"us_per_launch": us, "GBps": nbytes / (us * 1e-6) / 1e9,
+                         "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+                         "bytes_per_launch": nbytes}
+        _log(f"encoded rank chain {name}: {us:.1f} us, {results[name]['GBps']:.0f} GB/s")
+    results["workload"] = ("device rank-4 chain over an encoded boundary, 8192 states: "
+                           "finish (4 fitted ranks), commit (rank 3), requantize")
+    results["rotated_state_copies"] = ROTATIONS
+    del sets, nxt
+    return results
+
+
 CAPSULE_GEOMETRY = "0123456789abcdef" * 4
 SHA_BLOCKS_PER_CAPSULE = lambda p: (21624 + 1536 * p + 9 + 63) // 64  # noqa: E731
 
@@ -1003,6 +1094,7 @@ def profile_pass() -> int:
     bench_chunked_projection(1, 0)
     bench_window_step(0)
     bench_refit(1, 0)
+    bench_encoded_rank(1)
     bench_capsule(1, 0)
     torch.cuda.empty_cache()
     bench_pool(1, 0, "f32")
@@ -1084,6 +1176,8 @@ def main() -> int:
         extra["windowed_step"] = bench_window_step(args.warmup)
         torch.cuda.empty_cache()
         extra["window_refit"] = bench_refit(max(args.steps // 2, 5), 1)
+        torch.cuda.empty_cache()
+        extra["encoded_rank_chain"] = bench_encoded_rank(args.steps)
         torch.cuda.empty_cache()
         extra["capsule"] = bench_capsule(max(args.steps // 4, 3), args.warmup)
         if not args.no_cpu:
