@@ -43,6 +43,10 @@ C3_BYTES = 256 * 32 * 128 * 128 + 2 * 256 * 32 * 128 * 4 + 256 * 16 * 128 * 2 + 
 C4_BYTES = 64 * 32 * 128 * 128 + 2 * 64 * 32 * 128 * 4 + 64 * 64 * 32 * 128 * 2 + 64 * 64 * 32 * 128 * 4
 C4_FLOPS = 2 * 64 * 64 * 32 * 128 * 128
 ROTATIONS = 5
+# Back-to-back timing of the short kernels: warm-up and minimum timed launches
+# (the profile pass, which only needs a few launches per kernel, lowers them).
+WARM_MS, WARM_LAUNCHES = 100.0, 4000
+TIMED_MS, TIMED_LAUNCHES = 30.0, 1000
 PROBE_TILES = 65536
 PROBE_TILE_BYTES = PROBE_TILES * (128 * 128 * 4 + 128 * 128)
 
@@ -241,16 +245,25 @@ def _c1_style_state(shape, gen, dev):
 def _time_back_to_back(fn, calls, steps: int) -> float:
     """Microseconds per launch of `fn` over back-to-back launches cycling
     through the argument tuples `calls` (one per rotated state copy), between
-    one event pair: the per-step time of a loop issuing one projection after
+    one event pair: the per-step time of a loop issuing one launch after
     another.  The entry point is called with prepared arguments so that the
-    host keeps ahead of the GPU.  A warm phase of the same launches (at least
-    400, about 10 ms) first brings the GPU to its sustained clocks, which a
-    short timed region right after an idle host-side phase would not see."""
+    host keeps ahead of the GPU.  A warm phase of the same launches first
+    brings the GPU to its sustained clocks, which a short timed region right
+    after an idle host-side phase would not see (the clocks of 25 us kernels
+    were measured to keep rising for some 30 ms of continuous launches): about
+    WARM_MS of launches, at most WARM_LAUNCHES.  The timed region is at least
+    `steps` launches per copy and about TIMED_MS, at most TIMED_LAUNCHES."""
     import torch
 
-    for i in range(400):
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(20):
         assert fn(*calls[i % len(calls)]) == 0
-    n = max(steps * len(calls), 400)
+    b.record()
+    estimate_ms = max(_events_ms([(a, b)])[0] / 20, 1e-3)
+    for i in range(min(WARM_LAUNCHES, int(WARM_MS / estimate_ms) + 1)):
+        assert fn(*calls[i % len(calls)]) == 0
+    n = max(steps * len(calls), min(TIMED_LAUNCHES, int(TIMED_MS / estimate_ms) + 1))
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for i in range(n):
@@ -1081,11 +1094,22 @@ def codec_roofline(enc_ms: float, dec_ms: float) -> dict:
     return {**kernels[dominant], "dominant": True, "kernels": kernels}
 
 
+def _expand_probe_fraction(probe, dec_gbps: float) -> dict:
+    """The dequantize against the 1:4 read:write probe of the same run (the
+    faster of its plain and nontemporal forms): the ceiling of its traffic mix."""
+    if not probe:
+        return {}
+    ceiling = max(probe["expand_GBps"], probe["expand_nt_GBps"])
+    return {"expand_probe_GBps": ceiling, "frac_of_expand_probe": dec_gbps / ceiling}
+
+
 def profile_pass() -> int:
     """Two launches of each kernel at the benchmark shapes, and of the 4 GiB
     copy probe (the known-size reference for FETCH_SIZE / WRITE_SIZE)."""
     import torch
 
+    global WARM_LAUNCHES, TIMED_LAUNCHES
+    WARM_LAUNCHES, TIMED_LAUNCHES = 0, 1
     bench_codec(2, 0)
     torch.cuda.empty_cache()
     bench_hbm_probe(repeats=2)
@@ -1207,7 +1231,8 @@ def main() -> int:
                                "fp32 GDN state, layout [L,B,H,K,V]",
                    "tiles": C2_TILES, "bytes_per_direction": C2_BYTES},
         "quantize": {"ms": enc_ms, "GBps": enc_gbps, "hbm_frac": enc_gbps / HBM_PEAK_GBPS},
-        "dequantize": {"ms": dec_ms, "GBps": dec_gbps, "hbm_frac": dec_gbps / HBM_PEAK_GBPS},
+        "dequantize": {"ms": dec_ms, "GBps": dec_gbps, "hbm_frac": dec_gbps / HBM_PEAK_GBPS,
+                       **_expand_probe_fraction(extra.get("hbm_probe"), dec_gbps)},
         "roofline": codec_roofline(enc_ms, dec_ms),
         "cpu_baseline": cpu,
         **extra,
