@@ -109,6 +109,62 @@ __device__ __forceinline__ void store4(uint16_t* p, const float (&v)[4]) {
   stream_store(reinterpret_cast<uint2*>(p), q);
 }
 
+// The thread's 16 rows x 4 columns of a tile (row j at offset + j * 8 * 128
+// elements; the offset is unsigned so the loads can use a scalar base), widened
+// to fp32, and the smallest non-zero magnitude among them (INFINITY if all are
+// zero).
+//
+// fp32: on the bits, (b << 1) drops the sign and keeps the order of the
+// magnitudes, and subtracting 1 turns a zero into the largest unsigned value,
+// so one unsigned minimum (v_lshl_add + half a v_min3 per value) skips zeros.
+__device__ __forceinline__ float load_rows(const float* tile, uint32_t offset,
+                                           float (&x)[kRowsPerThread][4]) {
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) load4(tile + offset + j * 8 * kDim, x[j]);
+  uint32_t min_key = 0xFFFFFFFFu;
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; i += 2) {
+      const uint32_t a = (__float_as_uint(x[j][i]) << 1) - 1u;
+      const uint32_t b = (__float_as_uint(x[j][i + 1]) << 1) - 1u;
+      min_key = min(min_key, min(a, b));
+    }
+  }
+  return min_key == 0xFFFFFFFFu ? INFINITY : __uint_as_float((min_key + 1u) >> 1);
+}
+
+// bf16: on each packed pair, h * 0xFFFE mod 2^16 is 2^16 - 2|h| for a
+// non-zero h (the sign bit is shifted out) and 0 for +-0, so the largest key
+// belongs to the smallest non-zero magnitude: one v_pk_mul_lo_u16 and one
+// v_pk_max_u16 per two values.  The multiplier passes through an empty asm
+// statement so that the compiler keeps the single multiply instead of
+// rewriting it as a shift and a subtraction.
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float load_rows(const uint16_t* tile, uint32_t offset,
+                                           float (&x)[kRowsPerThread][4]) {
+  uint2 raw[kRowsPerThread];
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    raw[j] = stream_load(reinterpret_cast<const uint2*>(tile + offset + j * 8 * kDim));
+  }
+  u16x2_t multiplier = {0xFFFEu, 0xFFFEu};
+  asm("" : "+v"(multiplier));
+  u16x2_t best = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    best = __builtin_elementwise_max(best, __builtin_bit_cast(u16x2_t, raw[j].x) * multiplier);
+    best = __builtin_elementwise_max(best, __builtin_bit_cast(u16x2_t, raw[j].y) * multiplier);
+    x[j][0] = __uint_as_float(raw[j].x << 16);
+    x[j][1] = __uint_as_float(raw[j].x & 0xFFFF0000u);
+    x[j][2] = __uint_as_float(raw[j].y << 16);
+    x[j][3] = __uint_as_float(raw[j].y & 0xFFFF0000u);
+  }
+  const uint32_t key = max(static_cast<uint32_t>(best.x), static_cast<uint32_t>(best.y));
+  return key == 0u ? INFINITY : __uint_as_float(((0x10000u - key) >> 1) << 16);
+}
+
 // One reduce-scatter step over lane pairs (lane, lane ^ mask) for an array of
 // 2H partials: the lane whose `mask` bit is clear keeps the low half, its
 // partner the high half, and each adds the partner's copy of the half it keeps.
@@ -145,6 +201,13 @@ struct AddOp {
 struct MaxOp {
   __device__ __forceinline__ float operator()(float a, float b) const {
     return fmaxf(a, b);
+  }
+};
+// For operands known not to be NaN: equal to MaxOp there, and it needs no
+// canonicalize of shuffled operands.
+struct FiniteMaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const {
+    return __builtin_elementwise_maximum(a, b);
   }
 };
 
@@ -199,6 +262,107 @@ __device__ __forceinline__ void write_codes(const float (&x)[kRowsPerThread][4],
   }
 }
 
+// The same codes from two fmas and a fraction per value (code_lift and
+// code_byte_bits in codec_math.h), for finite m and scales in the reciprocal
+// division's domain.  A row of four values whose smallest lift fraction is
+// below the margin is recomputed on the exact path; that branch is divergent
+// and taken by about 3% of a wavefront's 256-value rows.
+template <uint32_t kLayout>
+__device__ __forceinline__ void write_codes_lifted(const float (&x)[kRowsPerThread][4],
+                                                   const float* scale_shared,
+                                                   const float* scale_inverse,
+                                                   const float* code_factor, int group,
+                                                   int c4, int8_t* out) {
+  float column_factor[4];
+  if constexpr (kLayout == kKeyValue) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) column_factor[i] = code_factor[4 * c4 + i];
+  }
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const float row_factor = kLayout == kKeyValue ? 0.0f : code_factor[8 * j + group];
+    uint32_t bits[4];
+    float fraction[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float factor = kLayout == kKeyValue ? column_factor[i] : row_factor;
+      fraction[i] = lift_fraction(code_lift(x[j][i], factor));
+      bits[i] = code_byte_bits(x[j][i], factor);
+    }
+    // The four low bytes into one word: two byte permutes and an or.
+    uint32_t packed = __builtin_amdgcn_perm(bits[1], bits[0], 0x0c0c0400u) |
+                      __builtin_amdgcn_perm(bits[3], bits[2], 0x04000c0cu);
+    if (fminf(fminf(fraction[0], fraction[1]), fminf(fraction[2], fraction[3])) <
+        kCodeLiftMargin) {
+      packed = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int value = kLayout == kKeyValue ? 4 * c4 + i : 8 * j + group;
+        const float q = div_by_reciprocal(x[j][i], scale_shared[value], scale_inverse[value]);
+        const int code = round_half_away_small(q * kQuantizedMaximum);
+        packed |= (static_cast<uint32_t>(code) & 0xFFu) << (8 * i);
+      }
+    }
+    // An unsigned 32-bit offset from the workgroup's base lets the store use the
+    // scalar-base addressing form instead of 64-bit vector address arithmetic.
+    const uint32_t offset = static_cast<uint32_t>((8 * j + group) * kDim + 4 * c4);
+    stream_store(reinterpret_cast<uint32_t*>(out + offset), packed);
+  }
+}
+
+// m = r / s in place (kFast: the reciprocal division), with the thread's
+// partial maxima of |m|: per row in the [value][key] layout (a row is one
+// value), per column over the thread's 16 rows in [key][value] (mx[0..3]).
+// On the fast path every m is finite, so the NaN-propagating maximum
+// (v_maximum3_f32 with abs modifiers, no canonicalize) equals fmaxf there; the
+// IEEE path keeps fmaxf, which like the reference's std::max skips NaNs.
+template <bool kFast>
+__device__ __forceinline__ float max_abs(float a, float b) {
+  if constexpr (kFast) {
+    return __builtin_elementwise_maximum(fabsf(a), fabsf(b));
+  } else {
+    return fmaxf(fabsf(a), fabsf(b));
+  }
+}
+
+template <uint32_t kLayout, bool kFast>
+__device__ __forceinline__ void smooth_and_max(float (&x)[kRowsPerThread][4],
+                                               const float* s_shared,
+                                               const float* s_inverse, int group,
+                                               int c4, float (&mx)[kRowsPerThread]) {
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
+      x[j][i] = kFast ? div_by_reciprocal(x[j][i], s_shared[key], s_inverse[key])
+                      : x[j][i] / s_shared[key];
+    }
+  }
+  if constexpr (kLayout == kKeyValue) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float m = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kRowsPerThread; j += 2) {
+        m = max_abs<kFast>(m, max_abs<kFast>(x[j][i], x[j + 1][i]));
+      }
+      mx[i] = m;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+      mx[j] = max_abs<kFast>(max_abs<kFast>(x[j][0], x[j][1]), max_abs<kFast>(x[j][2], x[j][3]));
+    }
+    // Row maxima over the half-wavefront: mx[0] of lane c holds row (c >> 1) & 15.
+    if constexpr (kFast) {
+      reduce_rows_over_half_wave(mx, c4, FiniteMaxOp{});
+    } else {
+      reduce_rows_over_half_wave(mx, c4, MaxOp{});
+    }
+  }
+}
+
 template <uint32_t kLayout, typename In, int kMode>
 __global__ __launch_bounds__(kThreads) void encode_kernel(
     const In* __restrict__ source, int8_t* __restrict__ codes,
@@ -211,6 +375,7 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   __shared__ float s_inverse[kDim];
   __shared__ float scale_shared[kDim];
   __shared__ float scale_inverse[kDim];
+  __shared__ float code_factor[kDim];
   __shared__ float min_part[4];
   __shared__ double tmax_part[4];
 
@@ -225,33 +390,16 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   const int c4 = t & 31;     // column quad
   const In* tile = source + entry * kTile;
 
+  // min_abs is the smallest NON-ZERO |r| of the thread's values: zeros add
+  // nothing to a key sum and divide exactly on both division paths, so they
+  // must not force the slow paths (dequantized states hold many exact zeros,
+  // one per code 0).
   float x[kRowsPerThread][4];
-#pragma unroll
-  for (int j = 0; j < kRowsPerThread; ++j) {
-    load4(tile + (8 * j + group) * kDim + 4 * c4, x[j]);
-  }
+  float min_abs = load_rows(tile, static_cast<uint32_t>(group * kDim + 4 * c4), x);
 
   bool fast_divide = false;
   if constexpr (kMode != kModeGivenSmoothing) {
     // ---- smoothing: per-key double sums of |r| ------------------------------
-    // min_abs is the smallest NON-ZERO |r|: zeros add nothing to a key sum and
-    // divide exactly on both division paths, so they must not force the slow
-    // paths (dequantized states hold many exact zeros, one per code 0).
-    // On the bits: (b << 1) drops the sign and keeps the order of the
-    // magnitudes, and subtracting 1 turns a zero into the largest unsigned
-    // value, so one unsigned minimum (v_lshl_add + half a v_min3 per value)
-    // skips the zeros.
-    uint32_t min_key = 0xFFFFFFFFu;
-#pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; i += 2) {
-        const uint32_t a = (__float_as_uint(x[j][i]) << 1) - 1u;
-        const uint32_t b = (__float_as_uint(x[j][i + 1]) << 1) - 1u;
-        min_key = min(min_key, min(a, b));
-      }
-    }
-    float min_abs = min_key == 0xFFFFFFFFu ? INFINITY : __uint_as_float((min_key + 1u) >> 1);
     if constexpr (kLayout == kKeyValue) {
       double p[kRowsPerThread];
 #pragma unroll
@@ -338,38 +486,17 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   }
   __syncthreads();
 
-  // ---- m = r / s -----------------------------------------------------------
+  // ---- m = r / s and the per-value scales max |m| over keys ----------------
   // The branch is uniform over the workgroup; each side is straight-line code.
+  float mx[kRowsPerThread];
   if (fast_divide) {
-#pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
-        x[j][i] = div_by_reciprocal(x[j][i], s_shared[key], s_inverse[key]);
-      }
-    }
+    smooth_and_max<kLayout, true>(x, s_shared, s_inverse, group, c4, mx);
   } else {
-#pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
-        x[j][i] = x[j][i] / s_shared[key];
-      }
-    }
+    smooth_and_max<kLayout, false>(x, s_shared, s_inverse, group, c4, mx);
   }
-
-  // ---- per-value scales: max |m| over keys --------------------------------
   if constexpr (kLayout == kKeyValue) {
-    float mx[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float m = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kRowsPerThread; ++j) m = fmaxf(m, fabsf(x[j][i]));
-      mx[i] = fmaxf(m, __shfl_xor(m, 32));
-    }
+    for (int i = 0; i < 4; ++i) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], 32));
     if (lane < 32) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) max_part[wave][4 * c4 + i] = mx[i];
@@ -380,13 +507,6 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
                               fmaxf(max_part[2][t], max_part[3][t]));
     }
   } else {
-    float mx[kRowsPerThread];
-#pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j) {
-      mx[j] = fmaxf(fmaxf(fabsf(x[j][0]), fabsf(x[j][1])),
-                    fmaxf(fabsf(x[j][2]), fabsf(x[j][3])));
-    }
-    reduce_rows_over_half_wave(mx, c4, MaxOp{});
     if ((c4 & 1) == 0) scale_shared[8 * ((c4 >> 1) & 15) + group] = mx[0];
   }
   __syncthreads();
@@ -394,6 +514,7 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   if (t < kDim) {
     const float scale = scale_shared[t];
     scale_inverse[t] = scale == 0.0f ? 0.0f : 1.0f / scale;
+    code_factor[t] = scale == 0.0f ? 0.0f : kQuantizedMaximum / scale;
     scales[item * kDim + t] = scale;
     scale_ok = scale == 0.0f || (scale >= 0x1p-90f && scale <= 0x1p90f);
   }
@@ -404,7 +525,9 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
 
   // ---- codes ---------------------------------------------------------------
   int8_t* out = codes + item * kTile;
-  if (fast_scale) {
+  if (fast_scale && fast_divide) {  // m finite: every r / s took the fast division
+    write_codes_lifted<kLayout>(x, scale_shared, scale_inverse, code_factor, group, c4, out);
+  } else if (fast_scale) {
     write_codes<kLayout, true>(x, scale_shared, scale_inverse, group, c4, out);
   } else {
     write_codes<kLayout, false>(x, scale_shared, scale_inverse, group, c4, out);

@@ -16,6 +16,15 @@
 //                                    [2^-100, 2^-99) and [2^99, 2^100], both signs)
 //   codec_math_check round           every float |x| <= 127: round_half_away_small(x)
 //                                    == clamp(lroundf(x), -127, 127)
+//   codec_math_check lift            the encoder's lifted codes: wherever
+//                                    lift_fraction(code_lift(m, RN(127/scale))) >=
+//                                    the margin, the low byte of code_byte_bits is
+//                                    clamp(lround(RN(RN(m/scale)*127)), -127, 127);
+//                                    every float m in [-scale, scale] for one
+//                                    scale, random scales in [2^-90, 2^90] with
+//                                    random m, and m within 200 ulps of every
+//                                    tie (n + 0.5) * scale / 127.  The count of
+//                                    values left to the exact path goes to stderr.
 // Prints "<checked> <failures>" and exits non-zero on any failure.
 #include <math.h>
 #include <stdint.h>
@@ -144,6 +153,86 @@ void check_round() {
   });
 }
 
+std::atomic<uint64_t> lift_fallbacks{0};
+
+// One lifted code against the reference expression; returns false on a
+// mismatch (a value whose lift fraction is below the margin is not a mismatch:
+// the kernel recomputes it exactly).
+bool lift_matches(float m, float scale, float factor, uint64_t& fallbacks) {
+  const float u = gdn::code_lift(m, factor);
+  if (!(gdn::lift_fraction(u) >= gdn::kCodeLiftMargin)) {
+    ++fallbacks;
+    return true;
+  }
+  const float scaled = scale == 0.0f ? 0.0f : m / scale * gdn::kQuantizedMaximum;
+  long expect = lroundf(scaled);
+  if (expect < -127) expect = -127;
+  if (expect > 127) expect = 127;
+  const int8_t got = static_cast<int8_t>(gdn::code_byte_bits(m, factor) & 0xFFu);
+  return got == static_cast<int8_t>(expect);
+}
+
+void check_lift_scale(float scale) {
+  const float factor = gdn::kQuantizedMaximum / scale;
+  const uint64_t end = static_cast<uint64_t>(to_bits(scale)) + 1;
+  parallel(0, end, [&](uint64_t u, uint64_t& n, uint64_t& bad) {
+    uint64_t fb = 0;
+    for (uint32_t sign = 0; sign < 2; ++sign) {
+      const float m = from_bits(static_cast<uint32_t>(u) | (sign << 31));
+      ++n;
+      if (!lift_matches(m, scale, factor, fb)) ++bad;
+    }
+    lift_fallbacks += fb;
+  });
+}
+
+uint32_t random_u32(uint64_t& state) {  // xorshift64*
+  state ^= state >> 12;
+  state ^= state << 25;
+  state ^= state >> 27;
+  return static_cast<uint32_t>((state * 0x2545F4914F6CDD1DULL) >> 32);
+}
+
+void check_lift() {
+  check_lift_scale(0.78539819f);
+  // Random scales over the fast domain; random m by bit pattern and by value,
+  // and m within 200 ulps of every tie point.
+  parallel(0, 2048, [&](uint64_t d, uint64_t& n, uint64_t& bad) {
+    uint64_t fb = 0;
+    uint64_t state = 0x9E3779B97F4A7C15ULL * (d + 1);
+    const uint32_t exponent = 127 - 90 + random_u32(state) % 181;
+    const float scale = from_bits((exponent << 23) | (random_u32(state) & 0x7FFFFFu));
+    const float factor = gdn::kQuantizedMaximum / scale;
+    for (int i = 0; i < 200000; ++i) {
+      const uint32_t bits = random_u32(state) % (to_bits(scale) + 1);
+      const float by_bits = from_bits(bits | ((random_u32(state) & 1u) << 31));
+      const float by_value = scale * (static_cast<float>(random_u32(state) >> 8) * 0x1p-24f) *
+                             ((random_u32(state) & 1u) ? -1.0f : 1.0f);
+      n += 2;
+      if (!lift_matches(by_bits, scale, factor, fb)) ++bad;
+      if (fabsf(by_value) <= scale && !lift_matches(by_value, scale, factor, fb)) ++bad;
+    }
+    for (int k = 0; k < 127; ++k) {
+      const float tie = (static_cast<float>(k) + 0.5f) / gdn::kQuantizedMaximum * scale;
+      for (int step = -200; step <= 200; ++step) {
+        const float m = from_bits(static_cast<uint32_t>(static_cast<int64_t>(to_bits(tie)) + step));
+        if (!(m <= scale)) continue;
+        n += 2;
+        if (!lift_matches(m, scale, factor, fb)) ++bad;
+        if (!lift_matches(-m, scale, factor, fb)) ++bad;
+      }
+    }
+    lift_fallbacks += fb;
+  });
+  // scale == 0: factor 0 and m == 0 give code 0.
+  uint64_t fb = 0;
+  checked += 2;
+  if (!lift_matches(0.0f, 0.0f, 0.0f, fb)) ++failures;
+  if (!lift_matches(-0.0f, 0.0f, 0.0f, fb)) ++failures;
+  lift_fallbacks += fb;
+  fprintf(stderr, "fallbacks %llu\n", static_cast<unsigned long long>(lift_fallbacks.load()));
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -156,6 +245,8 @@ int main(int argc, char** argv) {
     check_refit_domain();
   } else if (strcmp(argv[1], "round") == 0) {
     check_round();
+  } else if (strcmp(argv[1], "lift") == 0) {
+    check_lift();
   } else {
     return 2;
   }
