@@ -1,8 +1,10 @@
 // bf16 operands for v_mfma_f32_16x16x32_bf16 from int8 codes and fp32 values.
 //
-// Codes are exact in bf16 (the upper half of their exact fp32 value); fp32
-// values are split into three bf16 parts that sum to them exactly, so MFMA
-// products of codes and parts are exact and only the fp32 accumulation rounds.
+// Codes are exact in bf16 (the upper half of their exact fp32 value).  fp32
+// values are split into bf16 parts: three that sum to them exactly, or two
+// that leave a remainder below 2^-16 of the value.  MFMA products of a code
+// (7 significant bits) and a part (8) are exact, so only the split remainder
+// and the fp32 accumulation differ from the exact dot product.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -19,25 +21,19 @@ __device__ __forceinline__ uint32_t upper_halves(uint32_t first, uint32_t second
   return __builtin_amdgcn_perm(second, first, 0x07060302u);
 }
 
-// Three-way bf16 split of a pair of fp32 values, w = hi + mid + lo exactly,
-// by truncation: hi keeps the sign, exponent and top 7 fraction bits of w;
-// the remainder r = w - hi is exact in fp32 and has at most 16 significant
-// bits; mid keeps the top 8 of those and lo = r - mid, exact, has at most 8,
-// so every part is a bf16 value (the upper half of its fp32 pattern).
-__device__ __forceinline__ void split3_pair(float w0, float w1, uint32_t& hi,
-                                            uint32_t& mid, uint32_t& lo) {
-  constexpr uint32_t kUpper = 0xFFFF0000u;
-  const uint32_t h0 = __float_as_uint(w0) & kUpper;
-  const uint32_t h1 = __float_as_uint(w1) & kUpper;
-  const float r0 = w0 - __uint_as_float(h0);
-  const float r1 = w1 - __uint_as_float(h1);
-  const uint32_t m0 = __float_as_uint(r0) & kUpper;
-  const uint32_t m1 = __float_as_uint(r1) & kUpper;
-  const float t0 = r0 - __uint_as_float(m0);
-  const float t1 = r1 - __uint_as_float(m1);
-  hi = upper_halves(h0, h1);
-  mid = upper_halves(m0, m1);
-  lo = upper_halves(__float_as_uint(t0), __float_as_uint(t1));
+// Two-way bf16 split of a pair of fp32 values, rounding to nearest even
+// (one v_cvt_pk_bf16_f32 per part): hi = RN(w), lo = RN(w - hi), where
+// w - hi is exact in fp32.  |w - hi| <= 2^-8 |w| and |w - hi - lo| <= 2^-8
+// |w - hi| <= 2^-16 |w| (bf16 has 8 significant bits and fp32's exponent range,
+// so neither rounding underflows for |w| >= 2^-110).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void split2_pair(float w0, float w1, uint32_t& hi, uint32_t& lo) {
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){w0, w1}, bf16x2_t));
+  const float r0 = w0 - __uint_as_float(hi << 16);
+  const float r1 = w1 - __uint_as_float(hi & 0xFFFF0000u);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){r0, r1}, bf16x2_t));
 }
 
 // bf16 pair of the signed bytes 2*kPair, 2*kPair+1 of `word` (low element

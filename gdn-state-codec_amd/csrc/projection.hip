@@ -17,10 +17,15 @@
 //
 // Chunked (T queries per tile) is a [T x 128] x [128 x 128] contraction per
 // tile on bf16 MFMA (v_mfma_f32_16x16x32_bf16).  Codes are exact in bf16; the
-// fp32 operand w[t][k] = s[k] * x_t[k] is split into three bf16 parts
-// w = hi + mid + lo (exact), staged in LDS in the MFMA operand order, so the
-// products are exact and only fp32 accumulation rounds.  The scale[v] / 127
-// factor is applied in the epilogue.
+// fp32 operand w[t][k] = s[k] * x_t[k] is split into two bf16 parts
+// w ~ hi + lo (each rounded to nearest, remainder below 2^-16 |w|), staged in
+// LDS in the MFMA operand order.  The products with the codes are exact, so
+// the result differs from the exact readout by at most 2^-16 of sum |terms|
+// from the split plus the fp32 accumulation of 256 products (at most
+// 256 * 2^-24 of sum |terms|) and the epilogue's rounding: within
+// 2^-14 * sum |terms|.  The scale[v] / 127 factor is applied in the epilogue.
+// (A third part would make the products exact; it costs a third more MFMA
+// and LDS work and measured 7% slower at config 4.)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -189,8 +194,8 @@ __global__ __launch_bounds__(kThreads, 8) void decode_projection_kernel(
 // A workgroup owns one (sequence, head) tile; wavefront w owns the 32 values
 // 32w..32w+31 (two 16-column MFMA tiles) and keeps their codes in registers as
 // bf16 for every token block.  Token blocks of 16 rows are staged in LDS as the
-// three bf16 parts of w[t][k] = s[k] * x_t[k] in operand order (12 KiB), so
-// all 2048 workgroups of a 64 x 32-head batch are resident at once.
+// two bf16 parts of w[t][k] = s[k] * x_t[k] in operand order (8 KiB), so all
+// 2048 workgroups of a 64 x 32-head batch are resident at once.
 // The [value][key] form fits 64 VGPRs (8 wavefronts per SIMD); the byte gathers
 // of the [key][value] form need more.
 template <uint32_t kLayout>
@@ -200,7 +205,7 @@ __global__ __launch_bounds__(kThreads, kLayout == kValueKey ? 8 : 4) void chunke
     float* __restrict__ out, uint32_t tokens, uint32_t value_heads,
     uint32_t group, uint32_t query_heads, float query_scale) {
   constexpr int kBlockTokens = 16;
-  __shared__ uint4 a_lds[3][4][64];  // [split][k-step][lane] x 8 bf16
+  __shared__ uint4 a_lds[2][4][64];  // [part][k-step][lane] x 8 bf16
   __shared__ float s_lds[kDim];
   __shared__ __align__(16) float e_lds[kDim];  // scale[v] / 127
 
@@ -269,17 +274,16 @@ __global__ __launch_bounds__(kThreads, kLayout == kValueKey ? 8 : 4) void chunke
     const float4 s0 = *reinterpret_cast<const float4*>(s_lds + 8 * kc);
     const float4 s1 = *reinterpret_cast<const float4*>(s_lds + 8 * kc + 4);
     const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-    uint32_t hi[4], mid[4], lo[4];
+    uint32_t hi[4], lo[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const uint32_t word = word_of(qv, p);
       const float w0 = sv[2 * p] * (query_scale * bf16_to_float(word & 0xFFFFu));
       const float w1 = sv[2 * p + 1] * (query_scale * bf16_to_float(word >> 16));
-      split3_pair(w0, w1, hi[p], mid[p], lo[p]);
+      split2_pair(w0, w1, hi[p], lo[p]);
     }
     a_lds[0][dst_step][dst_lane] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-    a_lds[1][dst_step][dst_lane] = make_uint4(mid[0], mid[1], mid[2], mid[3]);
-    a_lds[2][dst_step][dst_lane] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    a_lds[1][dst_step][dst_lane] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
     __syncthreads();
 
     f32x4 acc[2];
@@ -288,8 +292,8 @@ __global__ __launch_bounds__(kThreads, kLayout == kValueKey ? 8 : 4) void chunke
 #pragma unroll
     for (int step = 0; step < 4; ++step) {
 #pragma unroll
-      for (int split = 0; split < 3; ++split) {
-        const bf16x8 a = __builtin_bit_cast(bf16x8, a_lds[split][step][lane]);
+      for (int part = 0; part < 2; ++part) {
+        const bf16x8 a = __builtin_bit_cast(bf16x8, a_lds[part][step][lane]);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[c][step], acc[c],
