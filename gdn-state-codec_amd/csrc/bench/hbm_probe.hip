@@ -6,9 +6,13 @@
 // with nontemporal accesses (the hint the codec kernels use).  They give the
 // bandwidth this GPU actually sustains, and the plain copy kernel is the
 // known-size reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings.
+// Each probe also runs in the XCD-contiguous order of the codec kernels
+// (xcd_contiguous_item in launch.h: XCD x streams the x-th eighth of the
+// buffer) beside the dispatcher's interleaved order.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "launch.h"
 #include "stream_memory.h"
 
 namespace {
@@ -33,41 +37,53 @@ __device__ __forceinline__ void store16(uint4* p, uint4 v) {
 constexpr int kThreads = 256;
 constexpr int kUnroll = 4;  // 16-byte accesses in flight per thread
 
-template <bool kNontemporal>
+template <bool kNontemporal, bool kXcd>
 __global__ __launch_bounds__(kThreads) void copy_kernel(const uint4* __restrict__ src,
                                                         uint4* __restrict__ dst,
                                                         uint64_t vectors) {
-  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads * kUnroll;
-  for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads * kUnroll +
-                       threadIdx.x;
-       base < vectors; base += stride) {
+  // Interleaved: the grid strides over the whole buffer.  XCD-contiguous:
+  // workgroup b (XCD b % 8) strides over the (b % 8)-th eighth with the
+  // workgroups of its XCD (the grid and the vector count are multiples of 8).
+  const uint64_t groups = kXcd ? gridDim.x / 8 : gridDim.x;
+  const uint64_t member = kXcd ? blockIdx.x / 8 : blockIdx.x;
+  const uint64_t begin = kXcd ? (blockIdx.x % 8) * (vectors / 8) : 0;
+  const uint64_t end = kXcd ? begin + vectors / 8 : vectors;
+  const uint64_t stride = groups * kThreads * kUnroll;
+  for (uint64_t base = begin + member * kThreads * kUnroll + threadIdx.x; base < end;
+       base += stride) {
     uint4 v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
-      if (i < vectors) v[u] = load16<kNontemporal>(src + i);
+      if (i < end) v[u] = load16<kNontemporal>(src + i);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
-      if (i < vectors) store16<kNontemporal>(dst + i, v[u]);
+      if (i < end) store16<kNontemporal>(dst + i, v[u]);
     }
   }
 }
 
-template <bool kNontemporal>
+template <bool kNontemporal, bool kXcd>
 __global__ __launch_bounds__(kThreads) void read_kernel(const uint4* __restrict__ src,
                                                         uint32_t* __restrict__ sink,
                                                         uint64_t vectors) {
-  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads * kUnroll;
+  // Interleaved: the grid strides over the whole buffer.  XCD-contiguous:
+  // workgroup b (XCD b % 8) strides over the (b % 8)-th eighth with the
+  // workgroups of its XCD (the grid and the vector count are multiples of 8).
+  const uint64_t groups = kXcd ? gridDim.x / 8 : gridDim.x;
+  const uint64_t member = kXcd ? blockIdx.x / 8 : blockIdx.x;
+  const uint64_t begin = kXcd ? (blockIdx.x % 8) * (vectors / 8) : 0;
+  const uint64_t end = kXcd ? begin + vectors / 8 : vectors;
+  const uint64_t stride = groups * kThreads * kUnroll;
   uint32_t acc = 0;
-  for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads * kUnroll +
-                       threadIdx.x;
-       base < vectors; base += stride) {
+  for (uint64_t base = begin + member * kThreads * kUnroll + threadIdx.x; base < end;
+       base += stride) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
-      if (i < vectors) {
+      if (i < end) {
         const uint4 v = load16<kNontemporal>(src + i);
         acc ^= v.x ^ v.y ^ v.z ^ v.w;
       }
@@ -77,19 +93,25 @@ __global__ __launch_bounds__(kThreads) void read_kernel(const uint4* __restrict_
   sink[static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x] = acc;
 }
 
-template <bool kNontemporal>
+template <bool kNontemporal, bool kXcd>
 __global__ __launch_bounds__(kThreads) void write_kernel(uint4* __restrict__ dst,
                                                          uint64_t vectors,
                                                          uint32_t value) {
-  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kThreads * kUnroll;
+  // Interleaved: the grid strides over the whole buffer.  XCD-contiguous:
+  // workgroup b (XCD b % 8) strides over the (b % 8)-th eighth with the
+  // workgroups of its XCD (the grid and the vector count are multiples of 8).
+  const uint64_t groups = kXcd ? gridDim.x / 8 : gridDim.x;
+  const uint64_t member = kXcd ? blockIdx.x / 8 : blockIdx.x;
+  const uint64_t begin = kXcd ? (blockIdx.x % 8) * (vectors / 8) : 0;
+  const uint64_t end = kXcd ? begin + vectors / 8 : vectors;
+  const uint64_t stride = groups * kThreads * kUnroll;
   const uint4 v = make_uint4(value, value, value, value);
-  for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * kThreads * kUnroll +
-                       threadIdx.x;
-       base < vectors; base += stride) {
+  for (uint64_t base = begin + member * kThreads * kUnroll + threadIdx.x; base < end;
+       base += stride) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const uint64_t i = base + static_cast<uint64_t>(u) * kThreads;
-      if (i < vectors) store16<kNontemporal>(dst + i, v);
+      if (i < end) store16<kNontemporal>(dst + i, v);
     }
   }
 }
@@ -106,10 +128,10 @@ __global__ __launch_bounds__(kThreads) void write_kernel(uint4* __restrict__ dst
 constexpr int kTileDim = 128;
 constexpr int kRowsPerThread = 16;
 
-template <bool kNontemporal>
+template <bool kNontemporal, bool kXcd>
 __global__ __launch_bounds__(kThreads) void expand_kernel(const uint32_t* __restrict__ src,
                                                           float4* __restrict__ dst) {
-  const uint64_t tile = blockIdx.x;
+  const uint64_t tile = kXcd ? gdn::xcd_contiguous_item(blockIdx.x, gridDim.x) : blockIdx.x;
   const int row0 = threadIdx.x >> 5;
   const int quad = threadIdx.x & 31;
   const uint32_t* in = src + tile * (kTileDim * kTileDim / 4);
@@ -135,10 +157,10 @@ __global__ __launch_bounds__(kThreads) void expand_kernel(const uint32_t* __rest
   }
 }
 
-template <bool kNontemporal>
+template <bool kNontemporal, bool kXcd>
 __global__ __launch_bounds__(kThreads) void contract_kernel(const uint4* __restrict__ src,
                                                             uint32_t* __restrict__ dst) {
-  const uint64_t tile = blockIdx.x;
+  const uint64_t tile = kXcd ? gdn::xcd_contiguous_item(blockIdx.x, gridDim.x) : blockIdx.x;
   const int row0 = threadIdx.x >> 5;
   const int quad = threadIdx.x & 31;
   const uint4* in = src + tile * (kTileDim * kTileDim / 4);
@@ -217,11 +239,11 @@ __global__ __launch_bounds__(kThreads) void valu_kernel(uint32_t* __restrict__ s
 // times over; the sink for the read probe must hold kProbeGrid * 256 words.
 extern "C" uint32_t gdn_hbm_probe_grid() { return 256u * 64u; }
 
-// mode 0: plain accesses; mode 1: nontemporal.
+// mode bit 0: nontemporal accesses; bit 1: XCD-contiguous order.
 extern "C" int32_t gdn_hbm_probe_copy(void* stream, const void* src, void* dst,
                                       uint64_t bytes, uint32_t mode) {
-  if (src == nullptr || dst == nullptr || bytes % 16 != 0 || mode > 1) return 1;
-  const auto kernel = mode ? copy_kernel<true> : copy_kernel<false>;
+  if (src == nullptr || dst == nullptr || bytes % 128 != 0 || mode > 3) return 1;
+  const auto kernel = mode == 0 ? copy_kernel<false, false> : mode == 1 ? copy_kernel<true, false> : mode == 2 ? copy_kernel<false, true> : copy_kernel<true, true>;
   hipLaunchKernelGGL(kernel, dim3(gdn_hbm_probe_grid()), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream),
                      static_cast<const uint4*>(src), static_cast<uint4*>(dst),
@@ -231,8 +253,8 @@ extern "C" int32_t gdn_hbm_probe_copy(void* stream, const void* src, void* dst,
 
 extern "C" int32_t gdn_hbm_probe_read(void* stream, const void* src, void* sink,
                                       uint64_t bytes, uint32_t mode) {
-  if (src == nullptr || sink == nullptr || bytes % 16 != 0 || mode > 1) return 1;
-  const auto kernel = mode ? read_kernel<true> : read_kernel<false>;
+  if (src == nullptr || sink == nullptr || bytes % 128 != 0 || mode > 3) return 1;
+  const auto kernel = mode == 0 ? read_kernel<false, false> : mode == 1 ? read_kernel<true, false> : mode == 2 ? read_kernel<false, true> : read_kernel<true, true>;
   hipLaunchKernelGGL(kernel, dim3(gdn_hbm_probe_grid()), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream),
                      static_cast<const uint4*>(src), static_cast<uint32_t*>(sink),
@@ -242,8 +264,8 @@ extern "C" int32_t gdn_hbm_probe_read(void* stream, const void* src, void* sink,
 
 extern "C" int32_t gdn_hbm_probe_write(void* stream, void* dst, uint64_t bytes,
                                        uint32_t mode) {
-  if (dst == nullptr || bytes % 16 != 0 || mode > 1) return 1;
-  const auto kernel = mode ? write_kernel<true> : write_kernel<false>;
+  if (dst == nullptr || bytes % 128 != 0 || mode > 3) return 1;
+  const auto kernel = mode == 0 ? write_kernel<false, false> : mode == 1 ? write_kernel<true, false> : mode == 2 ? write_kernel<false, true> : write_kernel<true, true>;
   hipLaunchKernelGGL(kernel, dim3(gdn_hbm_probe_grid()), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<uint4*>(dst),
                      bytes / 16, 0x3F800000u);
@@ -254,10 +276,10 @@ extern "C" int32_t gdn_hbm_probe_write(void* stream, void* dst, uint64_t bytes,
 // 64 KiB tiles of fp32 at dst (one workgroup per tile).
 extern "C" int32_t gdn_hbm_probe_expand(void* stream, const void* src, void* dst,
                                         uint64_t tiles, uint32_t mode) {
-  if (src == nullptr || dst == nullptr || tiles == 0 || tiles > 0x7FFFFFFFull || mode > 1) {
+  if (src == nullptr || dst == nullptr || tiles == 0 || tiles > 0x7FFFFFFFull || mode > 3) {
     return 1;
   }
-  const auto kernel = mode ? expand_kernel<true> : expand_kernel<false>;
+  const auto kernel = mode == 0 ? expand_kernel<false, false> : mode == 1 ? expand_kernel<true, false> : mode == 2 ? expand_kernel<false, true> : expand_kernel<true, true>;
   hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint32_t*>(src),
                      static_cast<float4*>(dst));
@@ -268,10 +290,10 @@ extern "C" int32_t gdn_hbm_probe_expand(void* stream, const void* src, void* dst
 // at dst (one workgroup per tile).
 extern "C" int32_t gdn_hbm_probe_contract(void* stream, const void* src, void* dst,
                                           uint64_t tiles, uint32_t mode) {
-  if (src == nullptr || dst == nullptr || tiles == 0 || tiles > 0x7FFFFFFFull || mode > 1) {
+  if (src == nullptr || dst == nullptr || tiles == 0 || tiles > 0x7FFFFFFFull || mode > 3) {
     return 1;
   }
-  const auto kernel = mode ? contract_kernel<true> : contract_kernel<false>;
+  const auto kernel = mode == 0 ? contract_kernel<false, false> : mode == 1 ? contract_kernel<true, false> : mode == 2 ? contract_kernel<false, true> : contract_kernel<true, true>;
   hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint4*>(src),
                      static_cast<uint32_t*>(dst));

@@ -6,6 +6,8 @@
 
 #include <tuple>
 
+#include "work_order.h"
+
 namespace gdn {
 
 // Status codes of every extern "C" entry point.  0 and 1 are the reference's

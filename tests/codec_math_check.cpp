@@ -25,6 +25,9 @@
 //                                    random m, and m within 200 ulps of every
 //                                    tie (n + 0.5) * scale / 127.  The count of
 //                                    values left to the exact path goes to stderr.
+//   codec_math_check order           xcd_contiguous_item (work_order.h) is a
+//                                    bijection on 0 .. n-1 for every n up to
+//                                    4096 and for the bench grids
 // Prints "<checked> <failures>" and exits non-zero on any failure.
 #include <math.h>
 #include <stdint.h>
@@ -37,6 +40,7 @@
 #include <vector>
 
 #include "codec_math.h"
+#include "work_order.h"
 
 namespace {
 
@@ -233,6 +237,29 @@ void check_lift() {
   fprintf(stderr, "fallbacks %llu\n", static_cast<unsigned long long>(lift_fallbacks.load()));
 }
 
+void check_order_grid(uint64_t blocks) {
+  std::vector<uint8_t> seen(blocks, 0);
+  bool ok = true;
+  for (uint64_t b = 0; b < blocks; ++b) {
+    const uint64_t item = gdn::xcd_contiguous_item(b, blocks);
+    if (item >= blocks || seen[item]) {
+      ok = false;
+      break;
+    }
+    seen[item] = 1;
+  }
+  ++checked;
+  if (!ok) ++failures;
+}
+
+void check_order() {
+  for (uint64_t n = 1; n <= 4096; ++n) check_order_grid(n);
+  // configs 2 and 5 (tiles), 3 and 4 (workgroups), odd sizes near them
+  for (uint64_t n : {245760ull, 491520ull, 2048ull, 8192ull, 245759ull, 245761ull, 491527ull}) {
+    check_order_grid(n);
+  }
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -247,6 +274,8 @@ int main(int argc, char** argv) {
     check_round();
   } else if (strcmp(argv[1], "lift") == 0) {
     check_lift();
+  } else if (strcmp(argv[1], "order") == 0) {
+    check_order();
   } else {
     return 2;
   }

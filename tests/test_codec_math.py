@@ -72,3 +72,10 @@ def test_lifted_codes_match_lround_wherever_the_margin_admits_them(checker):
     (about 3e5 mismatches), so the margin is what makes it pass."""
     rc, checked, failures = _run(checker, "lift")
     assert checked > 3_000_000_000 and failures == 0 and rc == 0
+
+
+def test_xcd_contiguous_order_is_a_bijection(checker):
+    """The streaming kernels' workgroup -> tile order (csrc/work_order.h) visits
+    every tile exactly once for every grid size up to 4,096 and the bench's."""
+    rc, checked, failures = _run(checker, "order")
+    assert checked == 4096 + 7 and failures == 0 and rc == 0
