@@ -93,16 +93,6 @@ __device__ __forceinline__ void load4<float>(const float* p, float (&v)[4]) {
   v[3] = q.w;
 }
 
-template <>
-__device__ __forceinline__ void load4<uint16_t>(const uint16_t* p,
-                                                float (&v)[4]) {
-  const uint2 q = stream_load(reinterpret_cast<const uint2*>(p));
-  v[0] = bf16_to_float(static_cast<uint16_t>(q.x & 0xFFFFu));
-  v[1] = bf16_to_float(static_cast<uint16_t>(q.x >> 16));
-  v[2] = bf16_to_float(static_cast<uint16_t>(q.y & 0xFFFFu));
-  v[3] = bf16_to_float(static_cast<uint16_t>(q.y >> 16));
-}
-
 __device__ __forceinline__ float load1(const float* p) { return *p; }
 __device__ __forceinline__ float load1(const uint16_t* p) {
   return bf16_to_float(*p);
