@@ -12,7 +12,9 @@
  * pairing of consecutive value heads on one query/key head
  * (kernel/gdn_state_codec_windowed_gdn_step.cpp:340).  Outputs are fp32 and
  * agree with the fp64 evaluation of the same sum to within
- * 2^-15 * (sum_k |code * s * x|) * scale / 127.
+ * 2^-15 * (sum_k |code * s * x|) * scale / 127 (decode) and 2^-14 times the
+ * same magnitude (chunked, whose weights s * x enter the bf16 matrix cores as
+ * two rounded bf16 parts).
  *
  * Same conventions as gdn_state_codec_kernel.h: asynchronous on `stream`, no
  * allocation, status 0 / 1 (bad argument) / 5 (launch failed).
