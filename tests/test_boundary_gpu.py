@@ -130,6 +130,40 @@ def test_power_refit_is_bit_exact(device, iterations):
     assert dw.cpu().numpy().tobytes() == ref_ws.tobytes()
 
 
+def test_power_refit_with_tiny_rows_is_bit_exact(device):
+    """States whose fitted residual has tiny rows (smoothing scaled by
+    2^-110, records and compensators zero: non-zero cells below 2^-100 and
+    a floored fresh smoothing), large rows (smoothing scaled by 2^10) and
+    rows alternating between tiny and ordinary in one state: the re-encode's
+    divisions, maxima and codes must be as bit-exact as for ordinary states.
+    (A fresh smoothing above 2^20 needs a mean |cell| above 2^40, which the
+    fp16 compensator factors cannot carry: such a state overflows them to
+    inf first.)"""
+    states = 48
+    print(f"power refit, tiny and mixed rows, states={states}", flush=True)
+    buf = WG.window_buffers(states, 91, VK, positions=16)
+    quiet = np.r_[0:16, 32:48]
+    for name in ("record_corrections", "compensator_keys", "compensator_values"):
+        buf[name][quiet] = 0
+    buf["smoothing"][0:16] *= np.float32(2.0 ** -110)
+    buf["smoothing"][16:32] *= np.float32(2.0 ** 10)
+    buf["smoothing"][32:48, ::2] *= np.float32(2.0 ** -110)
+    out = sentinel_outputs(states)
+    workspace = np.full((states, 128, 128), 7.0, np.float32)
+    d, do = to_device(buf, device), to_device(out, device)
+    dw = dev(workspace, device)
+    assert native().window_boundary_launch_v1(
+        stream(), *window_ptrs(d), *out_ptrs(do), dw.data_ptr(), states, 4) == 0
+    torch.cuda.synchronize()
+    ref, ref_out, ref_ws = WG.copy_buffers(buf), WG.copy_buffers(out), workspace.copy()
+    W.window_boundary_power(ref, ref_out, ref_ws, 4)
+    assert_same(from_device(do, out), ref_out, OUT_NAMES)
+    assert_same(from_device(d, buf), ref, buf.keys())
+    assert dw.cpu().numpy().tobytes() == ref_ws.tobytes()
+    tiny = np.abs(ref_ws[0:16])
+    assert ((tiny > 0) & (tiny < 2.0 ** -100)).any()  # the data reaches that range
+
+
 def _full_batch(seed):
     """B = 256 sequences x 32 value heads, the bench's refit batch: every
     seventeenth state is not full (positions 0..15 in turn) and must come back
