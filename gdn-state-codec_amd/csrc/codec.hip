@@ -27,6 +27,7 @@
 #include <stdint.h>
 
 #include "codec_math.h"
+#include "lane_exchange.h"
 #include "launch.h"
 #include "stream_memory.h"
 
@@ -167,31 +168,66 @@ __device__ __forceinline__ float load_rows(const uint16_t* tile, uint32_t offset
   return key == 0u ? INFINITY : __uint_as_float(((0x10000u - key) >> 1) << 16);
 }
 
-// One reduce-scatter step over lane pairs (lane, lane ^ mask) for an array of
-// 2H partials: the lane whose `mask` bit is clear keeps the low half, its
-// partner the high half, and each adds the partner's copy of the half it keeps.
-template <int H, typename T, typename Op>
-__device__ __forceinline__ void reduce_scatter_step(T* p, bool upper, int mask,
-                                                    Op op) {
+// Cross-lane exchanges.  Encodes of bf16 tiles (the slot pool's) exchange on
+// the VALU (DPP and permlane swaps, lane_exchange.h); fp32 tiles go through
+// ds_bpermute (__shfl_xor).  Measured on one box against the all-bpermute
+// kernel (ms): bf16 pool gather-encode 4.54 -> 4.39 with VALU exchanges; with
+// them, config-2 quantize went 3.14 -> 3.26 (its 64-bit key sums) and the fp32
+// pool gather-encode 6.24 -> 6.30.  Both forms combine the same operands.
+template <typename In>
+constexpr bool kExchangeOnValu = sizeof(In) == 2;
+
+// op(x, x of lane ^ kMask) in both lanes of the pair (op commutative).
+template <bool kValu, int kMask, typename T, typename Op>
+__device__ __forceinline__ T with_partner(T x, Op op) {
+  if constexpr (kValu) {
+    return combine_with_partner<kMask>(x, op);
+  } else {
+    return op(x, __shfl_xor(x, kMask));
+  }
+}
+
+// op over the 64 lanes, in every lane (op commutative and associative).
+template <bool kValu, typename T, typename Op>
+__device__ __forceinline__ T over_wave(T x, Op op) {
+  x = with_partner<kValu, 32>(x, op);
+  x = with_partner<kValu, 16>(x, op);
+  x = with_partner<kValu, 8>(x, op);
+  x = with_partner<kValu, 4>(x, op);
+  x = with_partner<kValu, 2>(x, op);
+  return with_partner<kValu, 1>(x, op);
+}
+
+// One reduce-scatter step over lane pairs (lane, lane ^ kMask) for an array of
+// 2H partials: the lane whose kMask bit is clear keeps the low half, its
+// partner the high half, and each combines the partner's copy of the half it
+// keeps.
+template <bool kValu, int H, int kMask, typename T, typename Op>
+__device__ __forceinline__ void reduce_scatter_step(T* p, int lane, Op op) {
 #pragma unroll
   for (int i = 0; i < H; ++i) {
-    const T send = upper ? p[i] : p[i + H];
-    const T keep = upper ? p[i + H] : p[i];
-    p[i] = op(keep, __shfl_xor(send, mask));
+    if constexpr (kValu) {
+      p[i] = fold_with<kMask>(p[i], p[i + H], lane, op);
+    } else {
+      const bool up = (lane & kMask) != 0;
+      const T send = up ? p[i] : p[i + H];
+      const T keep = up ? p[i + H] : p[i];
+      p[i] = op(keep, __shfl_xor(send, kMask));
+    }
   }
 }
 
 // Reduces 16 per-row partials over the 32 lanes of a half-wavefront.  Lane c
 // (c = lane % 32) ends holding, in p[0], the total of row (c >> 1) & 15; lanes
 // c and c ^ 1 hold the same value.
-template <typename T, typename Op>
+template <bool kValu, typename T, typename Op>
 __device__ __forceinline__ void reduce_rows_over_half_wave(T (&p)[16], int c,
                                                            Op op) {
-  reduce_scatter_step<8>(p, (c & 16) != 0, 16, op);
-  reduce_scatter_step<4>(p, (c & 8) != 0, 8, op);
-  reduce_scatter_step<2>(p, (c & 4) != 0, 4, op);
-  reduce_scatter_step<1>(p, (c & 2) != 0, 2, op);
-  p[0] = op(p[0], __shfl_xor(p[0], 1));
+  reduce_scatter_step<kValu, 8, 16>(p, c, op);
+  reduce_scatter_step<kValu, 4, 8>(p, c, op);
+  reduce_scatter_step<kValu, 2, 4>(p, c, op);
+  reduce_scatter_step<kValu, 1, 2>(p, c, op);
+  p[0] = with_partner<kValu, 1>(p[0], op);
 }
 
 struct AddOp {
@@ -203,6 +239,14 @@ struct AddOp {
 struct MaxOp {
   __device__ __forceinline__ float operator()(float a, float b) const {
     return fmaxf(a, b);
+  }
+  __device__ __forceinline__ double operator()(double a, double b) const {
+    return fmax(a, b);
+  }
+};
+struct MinOp {
+  __device__ __forceinline__ float operator()(float a, float b) const {
+    return fminf(a, b);
   }
 };
 // For operands known not to be NaN: equal to MaxOp there, and it needs no
@@ -264,11 +308,28 @@ __device__ __forceinline__ void write_codes(const float (&x)[kRowsPerThread][4],
   }
 }
 
-// The same codes from two fmas and a fraction per value (code_lift and
-// code_byte_bits in codec_math.h), for finite m and scales in the reciprocal
-// division's domain.  A row of four values whose smallest lift fraction is
-// below the margin is recomputed on the exact path; that branch is divergent
-// and taken by about 3% of a wavefront's 256-value rows.
+// floor of four lifts, each as the low byte of one word: v_cvt_flr_i32_f32
+// writes floor(u[0]) as an integer, and its SDWA form with dst_sel BYTE_k and
+// UNUSED_PRESERVE writes the low byte of floor(u[k]) into byte k and keeps the
+// other bytes.  For |u| < 2^31 the low byte of floor(u) is the two's-complement
+// byte of the code.
+__device__ __forceinline__ uint32_t pack_lifted_codes(const float (&u)[4]) {
+  uint32_t packed;
+  asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(packed) : "v"(u[0]));
+  asm("v_cvt_flr_i32_f32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD"
+      : "+v"(packed) : "v"(u[1]));
+  asm("v_cvt_flr_i32_f32_sdwa %0, %1 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD"
+      : "+v"(packed) : "v"(u[2]));
+  asm("v_cvt_flr_i32_f32_sdwa %0, %1 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD"
+      : "+v"(packed) : "v"(u[3]));
+  return packed;
+}
+
+// The same codes from one fma, a fraction and a floor per value (code_lift,
+// lift_fraction and lifted_code in codec_math.h), for finite m and scales in
+// the reciprocal division's domain.  A row of four values whose smallest lift
+// fraction is below the margin is recomputed on the exact path; that branch is
+// divergent and taken by about 3% of a wavefront's 256-value rows.
 template <uint32_t kLayout>
 __device__ __forceinline__ void write_codes_lifted(const float (&x)[kRowsPerThread][4],
                                                    const float* scale_shared,
@@ -283,17 +344,15 @@ __device__ __forceinline__ void write_codes_lifted(const float (&x)[kRowsPerThre
 #pragma unroll
   for (int j = 0; j < kRowsPerThread; ++j) {
     const float row_factor = kLayout == kKeyValue ? 0.0f : code_factor[8 * j + group];
-    uint32_t bits[4];
+    float lift[4];
     float fraction[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float factor = kLayout == kKeyValue ? column_factor[i] : row_factor;
-      fraction[i] = lift_fraction(code_lift(x[j][i], factor));
-      bits[i] = code_byte_bits(x[j][i], factor);
+      lift[i] = code_lift(x[j][i], factor);
+      fraction[i] = lift_fraction(lift[i]);
     }
-    // The four low bytes into one word: two byte permutes and an or.
-    uint32_t packed = __builtin_amdgcn_perm(bits[1], bits[0], 0x0c0c0400u) |
-                      __builtin_amdgcn_perm(bits[3], bits[2], 0x04000c0cu);
+    uint32_t packed = pack_lifted_codes(lift);
     if (fminf(fminf(fraction[0], fraction[1]), fminf(fraction[2], fraction[3])) <
         kCodeLiftMargin) {
       packed = 0;
@@ -327,7 +386,7 @@ __device__ __forceinline__ float max_abs(float a, float b) {
   }
 }
 
-template <uint32_t kLayout, bool kFast>
+template <uint32_t kLayout, bool kFast, bool kValu>
 __device__ __forceinline__ void smooth_and_max(float (&x)[kRowsPerThread][4],
                                                const float* s_shared,
                                                const float* s_inverse, int group,
@@ -358,9 +417,9 @@ __device__ __forceinline__ void smooth_and_max(float (&x)[kRowsPerThread][4],
     }
     // Row maxima over the half-wavefront: mx[0] of lane c holds row (c >> 1) & 15.
     if constexpr (kFast) {
-      reduce_rows_over_half_wave(mx, c4, FiniteMaxOp{});
+      reduce_rows_over_half_wave<kValu>(mx, c4, FiniteMaxOp{});
     } else {
-      reduce_rows_over_half_wave(mx, c4, MaxOp{});
+      reduce_rows_over_half_wave<kValu>(mx, c4, MaxOp{});
     }
   }
 }
@@ -381,6 +440,7 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   __shared__ float min_part[4];
   __shared__ double tmax_part[4];
 
+  constexpr bool kValu = kExchangeOnValu<In>;
   const uint64_t item = work_item(map);
   uint64_t entry;
   if (!pool_entry(map, item, &entry)) return;  // uniform over the workgroup
@@ -411,7 +471,7 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
                (static_cast<double>(fabsf(x[j][2])) +
                 static_cast<double>(fabsf(x[j][3])));
       }
-      reduce_rows_over_half_wave(p, c4, AddOp{});
+      reduce_rows_over_half_wave<kValu>(p, c4, AddOp{});
       if ((c4 & 1) == 0) key_sum[8 * ((c4 >> 1) & 15) + group] = p[0];
     } else {
       double p[4];
@@ -422,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
         for (int j = 0; j < kRowsPerThread; ++j) {
           acc += static_cast<double>(fabsf(x[j][i]));
         }
-        p[i] = acc + __shfl_xor(acc, 32);
+        p[i] = with_partner<kValu, 32>(acc, AddOp{});
       }
       if (lane < 32) {
 #pragma unroll
@@ -441,10 +501,8 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
     // 2^(e-23), so every partial sum below 2^(e+29) is a double without
     // rounding and any summation order gives the sequential sum.
     double tmax = t < kDim ? key_sum[t] : 0.0;
-    for (int mask = 32; mask >= 1; mask >>= 1) {
-      min_abs = fminf(min_abs, __shfl_xor(min_abs, mask));
-      tmax = fmax(tmax, __shfl_xor(tmax, mask));
-    }
+    min_abs = over_wave<kValu>(min_abs, MinOp{});
+    tmax = over_wave<kValu>(tmax, MaxOp{});
     if (lane == 0) {
       min_part[wave] = min_abs;
       tmax_part[wave] = tmax;
@@ -492,13 +550,13 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   // The branch is uniform over the workgroup; each side is straight-line code.
   float mx[kRowsPerThread];
   if (fast_divide) {
-    smooth_and_max<kLayout, true>(x, s_shared, s_inverse, group, c4, mx);
+    smooth_and_max<kLayout, true, kValu>(x, s_shared, s_inverse, group, c4, mx);
   } else {
-    smooth_and_max<kLayout, false>(x, s_shared, s_inverse, group, c4, mx);
+    smooth_and_max<kLayout, false, kValu>(x, s_shared, s_inverse, group, c4, mx);
   }
   if constexpr (kLayout == kKeyValue) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], 32));
+    for (int i = 0; i < 4; ++i) mx[i] = with_partner<kValu, 32>(mx[i], MaxOp{});
     if (lane < 32) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) max_part[wave][4 * c4 + i] = mx[i];

@@ -52,7 +52,8 @@ constexpr float kQuantizedMaximum = 127.0f;
 constexpr float kInvQuantizedMaximum = 1.0f / 127.0f;
 
 // The quant stage's code clamp(lround(p), -127, 127) with p = RN(RN(m / scale)
-// * 127) (state_capsule.cpp:213-219), from two fmas per value.  Preconditions:
+// * 127) (state_capsule.cpp:213-219), from one fma, a fraction and a floor per
+// value.  Preconditions:
 // |m| <= scale (scale is the maximum |m| of its column), m finite, and
 // factor = RN(127 / scale), or factor = 0 when scale == 0 (then m == 0).
 //
@@ -62,14 +63,11 @@ constexpr float kInvQuantizedMaximum = 1.0f / 127.0f;
 // 2^-14) adds at most 2^-18 (half an ulp below 128), so p + 0.5 lies within
 // 2^-15 of u - 2^-14.  If fract(u) >= 2^-13, then p + 0.5 and Y + 0.5 both lie
 // strictly between floor(u) and floor(u) + 1: neither is a tie, and the
-// integer nearest p, lround(p), equals the integer nearest Y.  That integer is
-// RN(Y + 1.5 * 2^23) - 1.5 * 2^23 (one fma: below 2^24 the grid spacing is 1),
-// and since 1.5 * 2^23 has zero low mantissa bits, the low byte of that sum's
-// bits is the code as a two's-complement byte.  |Y| < 127.5, so no clamp is
-// needed.  Values with fract(u) < 2^-13 (about 1 in 8,192) take the exact path.
+// integer nearest p, lround(p), equals the integer nearest Y, which is
+// floor(p + 0.5) = floor(u).  |Y| < 127.5, so no clamp is needed.  Values with
+// fract(u) < 2^-13 (about 1 in 8,192) take the exact path.
 constexpr float kCodeLiftOffset = 0.5f + 0x1p-14f;
 constexpr float kCodeLiftMargin = 0x1p-13f;
-constexpr float kCodeByteOffset = 0x1.8p23f;
 
 GDN_HD float code_lift(float m, float factor) { return fmaf(m, factor, kCodeLiftOffset); }
 
@@ -83,15 +81,9 @@ GDN_HD float lift_fraction(float u) {
 #endif
 }
 
-// Bits whose low byte is the code of m when its lift passed the margin.
-GDN_HD uint32_t code_byte_bits(float m, float factor) {
-  union {
-    float f;
-    uint32_t u;
-  } v;
-  v.f = fmaf(m, factor, kCodeByteOffset);
-  return v.u;
-}
+// The code of m when its lift u passed the margin: floor(u).  (The encoder
+// forms it with v_cvt_flr_i32_f32, which writes floor(u) as an integer.)
+GDN_HD int32_t lifted_code(float u) { return static_cast<int32_t>(floorf(u)); }
 
 // Reference smoothing floor (GdnStateCodecParameters::smoothing_floor,
 // gdn_state_codec_state_capsule.h:17).

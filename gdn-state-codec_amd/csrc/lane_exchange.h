@@ -124,6 +124,80 @@ __device__ __forceinline__ float add_partner(float x) {
   }
 }
 
+// 32- or 64-bit x of lane ^ kMask (kMask in 1, 2, 4, 8) by DPP; a 64-bit value
+// moves as two dwords.
+template <int kMask, typename T>
+__device__ __forceinline__ T dpp_xor(T x) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, from_lane_xor<kMask>(__builtin_bit_cast(int, x)));
+  } else {
+    const uint64_t bits = __builtin_bit_cast(uint64_t, x);
+    const uint32_t low = from_lane_xor<kMask>(static_cast<int>(static_cast<uint32_t>(bits)));
+    const uint32_t high = from_lane_xor<kMask>(static_cast<int>(static_cast<uint32_t>(bits >> 32)));
+    return __builtin_bit_cast(T, (static_cast<uint64_t>(high) << 32) | low);
+  }
+}
+
+// The two results of permlane{16,32}_swap(a, b) (kMask 16 or 32) for 32- or
+// 64-bit values, a 64-bit value as two dwords: a lane whose kMask bit is clear
+// gets its own a and its partner's a, a lane whose bit is set its partner's b
+// and its own b (in some order).
+template <int kMask, typename T>
+__device__ __forceinline__ void swap_with_partner(T a, T b, T& first, T& second) {
+  static_assert(kMask == 16 || kMask == 32, "permlane partner");
+  const auto swap = [](uint32_t x, uint32_t y, uint32_t& r0, uint32_t& r1) {
+    const auto r = kMask == 32 ? __builtin_amdgcn_permlane32_swap(x, y, false, false)
+                               : __builtin_amdgcn_permlane16_swap(x, y, false, false);
+    r0 = r[0];
+    r1 = r[1];
+  };
+  if constexpr (sizeof(T) == 4) {
+    uint32_t r0, r1;
+    swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), r0, r1);
+    first = __builtin_bit_cast(T, r0);
+    second = __builtin_bit_cast(T, r1);
+  } else {
+    static_assert(sizeof(T) == 8, "32- or 64-bit values");
+    const uint64_t x = __builtin_bit_cast(uint64_t, a);
+    const uint64_t y = __builtin_bit_cast(uint64_t, b);
+    uint32_t l0, l1, h0, h1;
+    swap(static_cast<uint32_t>(x), static_cast<uint32_t>(y), l0, l1);
+    swap(static_cast<uint32_t>(x >> 32), static_cast<uint32_t>(y >> 32), h0, h1);
+    first = __builtin_bit_cast(T, (static_cast<uint64_t>(h0) << 32) | l0);
+    second = __builtin_bit_cast(T, (static_cast<uint64_t>(h1) << 32) | l1);
+  }
+}
+
+// op(x, x of lane ^ kMask) for a commutative op, in both lanes of the pair.
+template <int kMask, typename T, typename Op>
+__device__ __forceinline__ T combine_with_partner(T x, Op op) {
+  if constexpr (kMask == 16 || kMask == 32) {
+    T first, second;
+    swap_with_partner<kMask>(x, x, first, second);
+    return op(first, second);
+  } else {
+    return op(x, dpp_xor<kMask>(x));
+  }
+}
+
+// fold for any commutative op and 32- or 64-bit values: a lane with the kMask
+// bit clear ends with op(lo, partner's lo), a lane with the bit set with
+// op(hi, partner's hi).
+template <int kMask, typename T, typename Op>
+__device__ __forceinline__ T fold_with(T lo, T hi, int lane, Op op) {
+  if constexpr (kMask == 16 || kMask == 32) {
+    T first, second;
+    swap_with_partner<kMask>(lo, hi, first, second);
+    return op(first, second);
+  } else {
+    const bool up = (lane & kMask) != 0;
+    const T send = up ? lo : hi;
+    const T keep = up ? hi : lo;
+    return op(keep, dpp_xor<kMask>(send));
+  }
+}
+
 // Sum over the 64 lanes, every lane receiving the same value (butterfly over
 // lane bits 32, 16, ..., 1).
 __device__ __forceinline__ float wave_sum_valu(float x) {

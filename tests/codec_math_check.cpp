@@ -18,7 +18,7 @@
 //                                    == clamp(lroundf(x), -127, 127)
 //   codec_math_check lift            the encoder's lifted codes: wherever
 //                                    lift_fraction(code_lift(m, RN(127/scale))) >=
-//                                    the margin, the low byte of code_byte_bits is
+//                                    the margin, lifted_code (its floor) is
 //                                    clamp(lround(RN(RN(m/scale)*127)), -127, 127);
 //                                    every float m in [-scale, scale] for one
 //                                    scale, random scales in [2^-90, 2^90] with
@@ -172,8 +172,7 @@ bool lift_matches(float m, float scale, float factor, uint64_t& fallbacks) {
   long expect = lroundf(scaled);
   if (expect < -127) expect = -127;
   if (expect > 127) expect = 127;
-  const int8_t got = static_cast<int8_t>(gdn::code_byte_bits(m, factor) & 0xFFu);
-  return got == static_cast<int8_t>(expect);
+  return gdn::lifted_code(u) == expect;
 }
 
 void check_lift_scale(float scale) {

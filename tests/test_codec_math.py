@@ -65,11 +65,11 @@ def test_rounding_matches_lround_for_every_float_up_to_127(checker):
 
 
 def test_lifted_codes_match_lround_wherever_the_margin_admits_them(checker):
-    """The encoder's two-fma code (code_lift / code_byte_bits in codec_math.h)
-    against clamp(lround(m / scale * 127)) in IEEE fp32: every float m of one
+    """The encoder's lifted code (floor of code_lift's fma, lifted_code in
+    codec_math.h) against clamp(lround(m / scale * 127)) in IEEE fp32: every float m of one
     scale, random scales over [2^-90, 2^90] with random m, and m within 200 ulps
     of every tie point.  With the margin lowered to 2^-20 this check fails
-    (about 3e5 mismatches), so the margin is what makes it pass."""
+    (about 1.3e7 mismatches), so the margin is what makes it pass."""
     rc, checked, failures = _run(checker, "lift")
     assert checked > 3_000_000_000 and failures == 0 and rc == 0
 
