@@ -7,8 +7,9 @@ Headline workload: one step = quantize + dequantize of a
 rotating over 5 distinct state copies so the 256 MB Infinity Cache cannot hold
 the working set.  Kernel durations come from HIP events recorded on the stream
 the kernels are launched on (torch's current stream).  The windowed decode
-step, its window-boundary refit, the capsule wire format (serialize /
-restore) and config 5 (the slot-indexed fp32 and bf16 pools) are reported
+step, its window-boundary refit, the encoded rank-4 chain, the capsule wire
+format (serialize / restore), the rank-4 boundary encode of the capsule
+factory and config 5 (the slot-indexed fp32 and bf16 pools) are reported
 beside the headline line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-pool]
@@ -708,6 +709,89 @@ def bench_encoded_rank(steps: int):
     return results
 
 
+def bench_boundary_fit(steps: int, cpu: bool):
+    """The capsule path's boundary encode with the rank-4 compensator fit
+    (quantize_boundary_launch_v1: FromDenseBoundary -> QuantizeBoundary,
+    state_capsule.cpp:129-226) on C1-style heads: 32 heads (config 1's size,
+    one round of workgroups) and 8,192 heads (a B=256 x 32-head layer), timed
+    back to back.  Its time is the fit's sequential chains (norms, the singular
+    value's 16,384-term sum), not HBM.  The CPU baseline runs the reference's
+    own QuantizeBoundary (oracle/_ref; the C restatement where _ref is absent)
+    over a bounded sample of the same heads, on one thread and on the host's
+    cores, and checks the GPU's codes and compensators on it bit for bit."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    import torch
+
+    import oracle
+    from gdn_state_codec import native
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(29)
+    heads = WINDOW_STATES
+    dense = _c1_style_state((heads, 128, 128), gen, dev)
+    out = {"residual": torch.empty_like(dense),
+           "codes": torch.empty((heads, 128, 128), dtype=torch.int8, device=dev),
+           "smoothing": torch.empty((heads, 128), device=dev),
+           "scales": torch.empty((heads, 128), device=dev),
+           "keys": torch.empty((heads, 128, 4), device=dev),
+           "values": torch.empty((heads, 128, 4), device=dev),
+           "status": torch.empty((heads,), dtype=torch.int32, device=dev)}
+    lib, stream = native(), torch.cuda.current_stream().cuda_stream
+    fn = lib.quantize_boundary_launch_v1
+
+    def call(n):
+        return (stream, dense.data_ptr(), *(out[k].data_ptr() for k in out), n, 4)
+
+    results = {"workload": "rank-4 boundary encode (fit + quant stage) of C1-style "
+                           "[key][value] heads", "rank": 4}
+    for n in (32, heads):
+        us = _time_back_to_back(fn, [call(n)], max(steps // 4, 2))
+        results[f"heads_{n}"] = {"ms_per_batch": us / 1e3, "heads_per_s": n / (us * 1e-6)}
+        _log(f"boundary fit: {n} heads in {us / 1e3:.3f} ms ({n / (us * 1e-6):.0f} heads/s)")
+    torch.cuda.synchronize()
+    assert int(out["status"].abs().sum()) == 0
+    if not cpu:
+        return results
+    kind = "reference" if oracle.ref_available() else "port"
+    fit = oracle.ref_quantize_kv if kind == "reference" else oracle.quantize_kv
+    x = dense.cpu().numpy()
+
+    def run(indices):
+        return [fit(x[i], rank=4) if kind == "reference" else fit(x[i], 4) for i in indices]
+
+    t0 = time.perf_counter()
+    run(range(8))
+    probe = (time.perf_counter() - t0) / 8
+    n = int(min(heads, max(8, 6.0 / max(probe, 1e-6))))
+    t0 = time.perf_counter()
+    single = run(range(n))
+    single_s = time.perf_counter() - t0
+    names = ("codes", "smoothing", "scales", "keys", "values")
+    gpu = {k: out[k][:n].cpu().numpy() for k in names}
+    exact = all(gpu[k][i].tobytes() == np.ascontiguousarray(single[i][j]).tobytes()
+                for i in range(n) for j, k in enumerate(names))
+    threads = _cpu_threads()
+    m = int(min(heads, n * threads))
+    bounds = np.linspace(0, m, threads + 1).astype(int)
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(threads) as pool:
+        list(pool.map(run, [range(lo, hi) for lo, hi in zip(bounds, bounds[1:])]))
+    multi_s = time.perf_counter() - t0
+    results["cpu_baseline"] = {
+        "value": m / multi_s, "unit": "heads/s", "cores": threads, "kind": kind,
+        "cpu_model": _cpu_model(), "seconds": multi_s,
+        "sample": f"the first {m} of the 8192 heads, split contiguously over {threads} threads",
+        "single_thread": {"value": n / single_s, "unit": "heads/s", "cores": 1,
+                          "sample": f"the first {n} heads", "seconds": single_s},
+        "gpu_bit_exact_on_sample": bool(exact)}
+    _log(f"cpu boundary fit ({kind}): {n / single_s:.1f} heads/s on 1 thread, "
+         f"{m / multi_s:.1f} heads/s on {threads} threads; GPU bit-exact={exact}")
+    return results
+
+
 CAPSULE_GEOMETRY = "0123456789abcdef" * 4
 SHA_BLOCKS_PER_CAPSULE = lambda p: (21624 + 1536 * p + 9 + 63) // 64  # noqa: E731
 
@@ -1135,6 +1219,8 @@ def profile_pass() -> int:
     bench_encoded_rank(1)
     bench_capsule(1, 0)
     torch.cuda.empty_cache()
+    bench_boundary_fit(1, False)
+    torch.cuda.empty_cache()
     bench_pool(1, 0, "f32")
     bench_pool(1, 0, "bf16")
     torch.cuda.synchronize()
@@ -1220,6 +1306,8 @@ def main() -> int:
         extra["capsule"] = bench_capsule(max(args.steps // 4, 3), args.warmup)
         if not args.no_cpu:
             extra["capsule"]["cpu_baseline"] = cpu_baseline_capsule()
+        torch.cuda.empty_cache()
+        extra["boundary_fit"] = bench_boundary_fit(args.steps, not args.no_cpu)
     if not args.no_pool and not args.only_codec:
         torch.cuda.empty_cache()
         extra["pool_codec"] = {

@@ -68,6 +68,47 @@ def encode(state: torch.Tensor, layout: int = LAYOUT_KEY_VALUE, codes=None,
     return codes, smoothing, scales
 
 
+FIT_STATUS = {1: "holds a non-finite value", 2: "has a non-finite compensator fit"}
+
+
+def quantize_boundary(dense: torch.Tensor, rank: int = 4, check: bool = True):
+    """The capsule factory's boundary encode (``FromDenseBoundary`` ->
+    ``QuantizeBoundary``, ``native/src/gdn_state_codec_state_capsule.cpp:129-226,
+    318-335``) of fp32 [...,128,128] [key][value] heads: the rank-``rank``
+    compensator fit, then the quant stage on the fitted residual.
+
+    Returns ``(codes, smoothing, scales, compensator_keys, compensator_values,
+    residual, status)``; the compensators are fp32 [...,128,rank].  With
+    ``check`` (the default) the call synchronizes and raises ``ValueError`` for
+    the first head the reference would reject (non-finite input or fit);
+    otherwise ``status`` (int32 per head: 0 ok, 1 non-finite input, 2
+    non-finite fit) is left for the caller to read."""
+    _require(0 <= rank <= 4, "GDN State Codec compensator rank must be 0..4")
+    heads = _tiles(dense, torch.float32, "dense boundary")
+    lead = tuple(dense.shape[:-2])
+    device = dense.device
+    codes = torch.empty(dense.shape, dtype=torch.int8, device=device)
+    smoothing = torch.empty(lead + (DIM,), dtype=torch.float32, device=device)
+    scales = torch.empty(lead + (DIM,), dtype=torch.float32, device=device)
+    keys = torch.empty(lead + (DIM, rank), dtype=torch.float32, device=device)
+    values = torch.empty(lead + (DIM, rank), dtype=torch.float32, device=device)
+    residual = torch.empty(dense.shape, dtype=torch.float32, device=device)
+    status = torch.empty(lead, dtype=torch.int32, device=device)
+    _check(native().quantize_boundary_launch_v1(
+        _stream(), dense.data_ptr(), residual.data_ptr(), codes.data_ptr(),
+        smoothing.data_ptr(), scales.data_ptr(), keys.data_ptr() if rank else 0,
+        values.data_ptr() if rank else 0, status.data_ptr(), heads, rank),
+        "quantize boundary")
+    if check:
+        flat = status.reshape(-1).cpu()
+        bad = torch.nonzero(flat).reshape(-1)
+        if bad.numel():
+            head = int(bad[0])
+            raise ValueError(f"GDN State Codec boundary head {head} "
+                             f"{FIT_STATUS.get(int(flat[head]), 'failed')}")
+    return codes, smoothing, scales, keys, values, residual, status
+
+
 def decode(codes: torch.Tensor, smoothing: torch.Tensor, scales: torch.Tensor,
            layout: int = LAYOUT_KEY_VALUE, compensator_keys=None,
            compensator_values=None, out=None) -> torch.Tensor:

@@ -96,6 +96,26 @@ int32_t statecentric_gdn_state_codec_encode_launch_v4(
     void* stream, const float* state, int8_t* quantized, float* smoothing,
     float* value_scales, uint64_t heads, uint32_t layout);
 
+/* The public capsule path's boundary encode for `heads` [key][value] fp32
+ * tiles: GdnStateCodecCapsule::FromDenseBoundary (state_capsule.cpp:318-335)
+ * through QuantizeBoundary (:129-226), i.e. the rank-`rank` compensator fit by
+ * power iteration from sinusoidal start vectors (:136-188), then the quant
+ * stage of encode_launch_v4 on the fitted residual, bit-identical to the
+ * reference's CPU code.  Outputs: residual (the fitted fp32 residual,
+ * [heads][128][128], also the quant stage's input), quantized [key][value],
+ * smoothing, value_scales, compensator_keys [heads][128][rank] and
+ * compensator_values [heads][128][rank] in fp32 (NULL allowed when rank is 0),
+ * and status[h]: 0, or 1 when head h holds a non-finite value (the reference
+ * rejects it before the fit), or 2 when a singular value is non-finite (the
+ * reference's check at :167-169); a head with a non-zero status has
+ * unspecified outputs.  0 <= rank <= 4 (the capsule schema fixes 4),
+ * 1 <= heads <= 2^31-1.  The reference exposes this only as the C++ capsule
+ * factory; this batched entry point has no C-ABI counterpart. */
+int32_t statecentric_gdn_state_codec_quantize_boundary_launch_v1(
+    void* stream, const float* dense, float* residual, int8_t* quantized,
+    float* smoothing, float* value_scales, float* compensator_keys,
+    float* compensator_values, int32_t* status, uint64_t heads, uint32_t rank);
+
 /* Decode of `heads` tiles.  compensator_keys/values are both NULL (quant-only,
  * rank 0) or both fp32 [heads][128][4] (rank 4, the dequantize_launch_v1 form). */
 int32_t statecentric_gdn_state_codec_decode_launch_v4(

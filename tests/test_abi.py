@@ -194,6 +194,22 @@ def test_encoded_rank_chain_admits_like_the_reference(lib):
         assert lib.encoded_requantize_launch_v1(None, *args, 8) == 1
 
 
+def test_quantize_boundary_admission(lib):
+    """The rank-r boundary encode: every pointer required except the
+    compensators at rank 0, 1 <= heads <= 2^31-1 and rank <= 4; all rejected
+    before any HIP call."""
+    p = ctypes.c_void_p(16)
+    eight = [p] * 8
+    for heads, rank in ((0, 4), (1 << 31, 4), (2, 5)):
+        assert lib.quantize_boundary_launch_v1(None, *eight, heads, rank) == 1
+    for i in range(8):
+        args = list(eight)
+        args[i] = None
+        assert lib.quantize_boundary_launch_v1(None, *args, 2, 4) == 1
+        if i not in (5, 6):  # the compensators may be null at rank 0
+            assert lib.quantize_boundary_launch_v1(None, *args, 2, 0) == 1
+
+
 def test_noalloc_refit_admission(lib):
     """The allocation-free refit: every pointer required, at most 512 states
     when the power refit needs the scratch workspace, 16384 without it, and
@@ -297,6 +313,7 @@ _ALIGNMENT_CASES = {
     "boundary_scale_records_launch_v1": [None] + ["P"] * 3 + [2],
     "window_boundary_cube_finish_launch_v1": [None] + ["P"] * 15 + [2],
     "bf16_cube_matmul_launch_v1": [None, "P", "P", "P", 2, 16, 16, 1],
+    "quantize_boundary_launch_v1": [None] + ["P"] * 8 + [2, 4],
     "capsule_serialize_launch_v1": [None] + ["P"] * 9 + [1, _GEOMETRY, 1, 1, "P", "P", 1 << 20,
                                                           "P", 2],
     "capsule_restore_launch_v1": [None, "P", "P", "P", 1 << 20, _GEOMETRY, 1, 1, "P", 1]
