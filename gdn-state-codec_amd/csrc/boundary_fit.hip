@@ -18,18 +18,24 @@
 //
 // One 128-thread workgroup per head.  The residual lives in LDS at a row
 // stride of 129 floats, so a thread per row (left = R right) and a thread per
-// column (right = R^T left) both read it without bank conflicts.  The norms
-// and the singular value are single-thread chains, as the reference's order
-// requires; the sums of the two products run one per thread.
+// column (right = R^T left) both read it without bank conflicts.  Each of
+// those sums runs on its own thread with its 128 loads unrolled ahead of the
+// chain.  Every thread evaluates each norm identically from LDS (no broadcast,
+// one barrier fewer) and writes its normalized element to the vector's other
+// buffer.  The singular value's 16,384 products are formed in parallel, one row
+// per thread in registers, and summed in the reference's order by a relay:
+// row r's thread adds its 128 products to the total of rows 0..r-1.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
 
 #include <cfloat>
 #include <cmath>
+#include <type_traits>
 
 #include "gdn_state_codec_kernel.h"
 #include "launch.h"
+#include "window_common.h"
 
 namespace gdn {
 namespace {
@@ -61,39 +67,50 @@ struct FitArgs {
 
 struct FitShared {
   float r[kDim * kRowStride];
+  float raw[kDim];     // a matrix-vector product before its normalization
   float left[kDim];
   float right[kDim];
-  float scalar;
-  int flag;
+  float total;         // the singular value's running sum
 };
 
-// Normalize (:60-65) of v[0..127] with the reference's Norm: thread 0 forms
-// the sequential double sum of squares (each square exact in double) and its
-// double square root; every thread divides its own element.
-__device__ bool normalize(FitShared& sh, float* v, int t) {
-  if (t == 0) {
-    double sum = 0.0;
-    for (int i = 0; i < kDim; ++i) {
-      const double x = static_cast<double>(v[i]);
-      sum += x * x;
-    }
-    const float norm = static_cast<float>(sqrt(sum));
-    sh.flag = norm > FLT_EPSILON ? 1 : 0;
-    sh.scalar = norm;
+// f(std::integral_constant<int, i>) for i = 0 .. kCount - 1, expanded at
+// compile time, so that register arrays indexed by i stay in VGPRs and the
+// loads of a whole sum can be issued ahead of its dependent chain.
+template <int kCount, int kIndex = 0, typename F>
+__device__ __forceinline__ void unrolled(F&& f) {
+  if constexpr (kIndex < kCount) {
+    f(std::integral_constant<int, kIndex>{});
+    unrolled<kCount, kIndex + 1>(f);
   }
-  __syncthreads();
-  const bool ok = sh.flag != 0;
-  if (ok) v[t] = v[t] / sh.scalar;
-  __syncthreads();
+}
+
+// Normalize (:60-65) of raw[0..127] into out[]: the reference's Norm, a
+// sequential double sum of squares (each square exact in double) and a
+// double square root rounded to float, evaluated identically by every thread;
+// each thread then writes its own element, divided when the norm exceeds
+// FLT_EPSILON and copied unchanged otherwise (Normalize leaves the vector as
+// it was).  The caller has made raw[] visible; the caller's next barrier
+// publishes out[].
+__device__ __forceinline__ bool normalize_into(const float* raw, float* out, int t) {
+  double sum = 0.0;
+  unrolled<kDim>([&](auto i) {
+    const double x = static_cast<double>(raw[decltype(i)::value]);
+    sum += x * x;
+  });
+  const float norm = static_cast<float>(sqrt(sum));
+  const bool ok = norm > FLT_EPSILON;
+  out[t] = ok ? raw[t] / norm : raw[t];
   return ok;
 }
 
-__global__ __launch_bounds__(kFitThreads) void boundary_fit_kernel(FitArgs a, StartVectors start) {
+__global__ __launch_bounds__(kFitThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void boundary_fit_kernel(FitArgs a, StartVectors start) {
   extern __shared__ __align__(16) unsigned char dynamic[];
   FitShared& sh = *reinterpret_cast<FitShared*>(dynamic);
   const int t = threadIdx.x;
   const uint64_t head = blockIdx.x;
   const float* const dense = a.dense + head * kTile;
+  float* const my_row = sh.r + t * kRowStride;
 
   bool finite = true;
   for (int row = 0; row < kDim; ++row) {
@@ -107,41 +124,58 @@ __global__ __launch_bounds__(kFitThreads) void boundary_fit_kernel(FitArgs a, St
   }
 
   for (uint32_t rank = 0; rank < a.rank; ++rank) {
-    sh.right[t] = start.value[rank][t];
+    sh.raw[t] = start.value[rank][t];
     __syncthreads();
-    if (!normalize(sh, sh.right, t)) {
-      if (t == 0) sh.right[0] = 1.0f;
-      __syncthreads();
-    }
+    if (!normalize_into(sh.raw, sh.right, t) && t == 0) sh.right[0] = 1.0f;
+    __syncthreads();
     for (int iteration = 0; iteration < kFitIterations; ++iteration) {
       {  // left[row] = sum over columns of R[row][col] * right[col] (thread = row)
-        const float* row = sh.r + t * kRowStride;
         float acc = 0.0f;
-        for (int column = 0; column < kDim; ++column) acc += row[column] * sh.right[column];
-        sh.left[t] = acc;
+        unrolled<kDim>([&](auto c) {
+          constexpr int column = decltype(c)::value;
+          acc += my_row[column] * sh.right[column];
+        });
+        sh.raw[t] = acc;
       }
       __syncthreads();
-      if (!normalize(sh, sh.left, t)) break;
+      const bool left_ok = normalize_into(sh.raw, sh.left, t);
+      __syncthreads();
+      if (!left_ok) break;  // uniform: every thread formed the same norm
       {  // right[col] = sum over rows of R[row][col] * left[row] (thread = column)
         float acc = 0.0f;
-        for (int row = 0; row < kDim; ++row) acc += sh.r[row * kRowStride + t] * sh.left[row];
-        sh.right[t] = acc;
+        unrolled<kDim>([&](auto r) {
+          constexpr int row = decltype(r)::value;
+          acc += sh.r[row * kRowStride + t] * sh.left[row];
+        });
+        sh.raw[t] = acc;
       }
       __syncthreads();
-      if (!normalize(sh, sh.right, t)) break;
+      const bool right_ok = normalize_into(sh.raw, sh.right, t);
+      __syncthreads();
+      if (!right_ok) break;
     }
-    // Singular value: one sequential sum over rows, then columns (:160-166).
-    if (t == 0) {
-      float singular = 0.0f;
-      for (int row = 0; row < kDim; ++row) {
-        const float l = sh.left[row];
-        const float* r = sh.r + row * kRowStride;
-        for (int column = 0; column < kDim; ++column) singular += l * r[column] * sh.right[column];
+    // Singular value (:160-166): thread t forms row t's products
+    // (left[t] * R[t][col]) * right[col]; the relay then adds them in the
+    // reference's order, rows 0..127, columns 0..127 within each row.
+    float product[kDim];
+    {
+      const float l = sh.left[t];
+      unrolled<kDim>([&](auto c) {
+        constexpr int column = decltype(c)::value;
+        product[column] = l * my_row[column] * sh.right[column];
+      });
+    }
+    for (int row = 0; row < kDim; ++row) {
+      if (row == kDim / 2) __syncthreads();  // the relay passes from wavefront 0 to 1
+      if (t == row) {
+        float total = row == 0 ? 0.0f : sh.total;
+        unrolled<kDim>([&](auto c) { total += product[decltype(c)::value]; });
+        sh.total = total;
       }
-      sh.scalar = singular;
+      wave_lds_sync();  // lane row's total before lane row + 1 reads it
     }
     __syncthreads();
-    const float singular = sh.scalar;
+    const float singular = sh.total;
     if (!isfinite(singular)) {  // uniform
       if (t == 0) a.status[head] = kFitNonFiniteSingular;
       return;
@@ -149,10 +183,11 @@ __global__ __launch_bounds__(kFitThreads) void boundary_fit_kernel(FitArgs a, St
     const float key = sh.left[t] * singular;
     a.comp_keys[(head * kDim + t) * a.rank + rank] = key;
     a.comp_values[(head * kDim + t) * a.rank + rank] = sh.right[t];
-    {  // R[row][col] -= left[row] * sv * right[col] (thread = row)
-      float* row = sh.r + t * kRowStride;
-      for (int column = 0; column < kDim; ++column) row[column] -= key * sh.right[column];
-    }
+    // R[row][col] -= left[row] * sv * right[col] (thread = row)
+    unrolled<kDim>([&](auto c) {
+      constexpr int column = decltype(c)::value;
+      my_row[column] -= key * sh.right[column];
+    });
     __syncthreads();
   }
 
