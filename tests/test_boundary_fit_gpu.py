@@ -2,8 +2,8 @@
 fit (quantize_boundary_launch_v1; FromDenseBoundary -> QuantizeBoundary,
 native/src/gdn_state_codec_state_capsule.cpp:129-226, 318-335): bit-exact
 against the outputs the reference's own C++ wrote for the golden heads and
-against the C oracle (pinned to that C++ at rank 0 and 4 by
-test_oracle_reference.py) at every rank, through the C-ABI."""
+against the C oracle (pinned to that C++ at every rank 0..4 by
+test_oracle_reference.py), through the C-ABI."""
 
 from pathlib import Path
 

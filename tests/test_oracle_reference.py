@@ -32,7 +32,7 @@ def _cases():
     yield 102, datagen.huge_head(7)
 
 
-@pytest.mark.parametrize("rank", [0, 4])
+@pytest.mark.parametrize("rank", [0, 1, 2, 3, 4])
 def test_quantize_dequantize_readout_match_reference(rank):
     g = datagen.rng(11)
     for i, x in _cases():
