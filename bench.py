@@ -9,8 +9,8 @@ the working set.  Kernel durations come from HIP events recorded on the stream
 the kernels are launched on (torch's current stream).  The windowed decode
 step, its window-boundary refit, the encoded rank-4 chain, the capsule wire
 format (serialize / restore), the rank-4 boundary encode of the capsule
-factory and config 5 (the slot-indexed fp32 and bf16 pools) are reported
-beside the headline line.
+factory, config 1 (the 32-head round trip) and config 5 (the slot-indexed fp32
+and bf16 pools) are reported beside the headline line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-pool]
 
@@ -709,6 +709,88 @@ def bench_encoded_rank(steps: int):
     return results
 
 
+def bench_config1(steps: int, cpu: bool):
+    """Config 1, the reference's CPU-runnable case: quantize + dequantize of 32
+    C1-style [key][value] heads (2 MiB in).  The GPU round trip is timed back to
+    back; the CPU baseline is the reference's own C++ (oracle/_ref; the C
+    restatement where _ref is absent) on the same 32 heads, 3 warm-ups then the
+    median of 11 repetitions, on one thread and with the heads split over the
+    host's cores, and the GPU's codes are checked against it bit for bit."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    import torch
+
+    import oracle
+    from gdn_state_codec import native
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(31)
+    heads = 32
+    state = _c1_style_state((heads, 128, 128), gen, dev)
+    codes = torch.empty(state.shape, dtype=torch.int8, device=dev)
+    smoothing = torch.empty((heads, 128), device=dev)
+    scales = torch.empty((heads, 128), device=dev)
+    dense = torch.empty_like(state)
+    lib, stream = native(), torch.cuda.current_stream().cuda_stream
+
+    def round_trip_gpu():
+        status = lib.encode_launch_v4(stream, state.data_ptr(), codes.data_ptr(),
+                                      smoothing.data_ptr(), scales.data_ptr(), heads, 0)
+        return status or lib.decode_launch_v4(stream, codes.data_ptr(), smoothing.data_ptr(),
+                                              scales.data_ptr(), None, None, dense.data_ptr(),
+                                              heads, 0)
+
+    us = _time_back_to_back(lambda: round_trip_gpu(), [()], steps)
+    nbytes = 2 * heads * (128 * 128 * 5 + 2 * 128 * 4)
+    results = {"workload": "config 1: quantize + dequantize of 32 C1-style [key][value] heads",
+               "us_per_round_trip": us, "GBps": nbytes / (us * 1e-6) / 1e9,
+               "bytes_per_round_trip": nbytes}
+    _log(f"config 1: {heads} heads round trip in {us:.1f} us")
+    if not cpu:
+        return results
+    kind = "reference" if oracle.ref_available() else "port"
+    x = state.cpu().numpy()
+
+    def round_trip_cpu(part):
+        if kind == "reference":
+            c, s, sc = oracle.ref_quantize_heads(part)
+            oracle.ref_dequantize_heads(c, s, sc)
+        else:
+            c, s, sc = oracle.encode_heads(part, oracle.LAYOUT_KEY_VALUE, threads=1)
+            oracle.decode_heads(c, s, sc, oracle.LAYOUT_KEY_VALUE, threads=1)
+        return c
+
+    def median_seconds(fn):
+        for _ in range(3):
+            fn()
+        times = []
+        for _ in range(11):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times))
+
+    single = median_seconds(lambda: round_trip_cpu(x))
+    threads = _cpu_threads()
+    bounds = np.linspace(0, heads, threads + 1).astype(int)
+    pool = ThreadPoolExecutor(threads)
+    multi = median_seconds(lambda: list(pool.map(
+        round_trip_cpu, [x[lo:hi] for lo, hi in zip(bounds, bounds[1:]) if hi > lo])))
+    pool.shutdown()
+    torch.cuda.synchronize()
+    exact = codes.cpu().numpy().tobytes() == round_trip_cpu(x).tobytes()
+    results["cpu_baseline"] = {
+        "value": multi * 1e6, "unit": "us per round trip", "cores": threads, "kind": kind,
+        "cpu_model": _cpu_model(), "sample": "the same 32 heads, median of 11 after 3 warm-ups",
+        "single_thread": {"value": single * 1e6, "unit": "us per round trip", "cores": 1},
+        "gpu_codes_bit_exact": bool(exact)}
+    _log(f"cpu config 1 ({kind}): {single * 1e6:.0f} us on 1 thread, {multi * 1e6:.0f} us on "
+         f"{threads} threads; GPU codes bit-exact={exact}")
+    return results
+
+
 def bench_boundary_fit(steps: int, cpu: bool):
     """The capsule path's boundary encode with the rank-4 compensator fit
     (quantize_boundary_launch_v1: FromDenseBoundary -> QuantizeBoundary,
@@ -1308,6 +1390,7 @@ def main() -> int:
             extra["capsule"]["cpu_baseline"] = cpu_baseline_capsule()
         torch.cuda.empty_cache()
         extra["boundary_fit"] = bench_boundary_fit(args.steps, not args.no_cpu)
+        extra["config1"] = bench_config1(args.steps, not args.no_cpu)
     if not args.no_pool and not args.only_codec:
         torch.cuda.empty_cache()
         extra["pool_codec"] = {
