@@ -744,10 +744,13 @@ def bench_config1(steps: int, cpu: bool):
 
     us = _time_back_to_back(lambda: round_trip_gpu(), [()], steps)
     nbytes = 2 * heads * (128 * 128 * 5 + 2 * 128 * 4)
+    error = (dense.double() - state.double())
+    mse = float(error.square().mean())
     results = {"workload": "config 1: quantize + dequantize of 32 C1-style [key][value] heads",
                "us_per_round_trip": us, "GBps": nbytes / (us * 1e-6) / 1e9,
-               "bytes_per_round_trip": nbytes}
-    _log(f"config 1: {heads} heads round trip in {us:.1f} us")
+               "bytes_per_round_trip": nbytes, "mse": mse,
+               "relative_rms": (mse / float(state.double().square().mean())) ** 0.5}
+    _log(f"config 1: {heads} heads round trip in {us:.1f} us, mse {mse:.3e}")
     if not cpu:
         return results
     kind = "reference" if oracle.ref_available() else "port"
