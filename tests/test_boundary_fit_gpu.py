@@ -115,3 +115,22 @@ def test_fitted_residual_is_what_the_quant_stage_encodes(device):
     assert host(plain[1]).tobytes() == host(s).tobytes()
     fit = np.einsum("hkr,hvr->hkv", host(ck).astype(np.float64), host(cv).astype(np.float64))
     assert np.abs(host(residual) - (heads - fit)).max() < 1e-5 * np.abs(heads).max()
+
+
+def test_boundary_encode_over_several_rounds_of_workgroups(device):
+    """1,536 heads (three times what the GPU holds at once): every status 0,
+    and every 97th head bit-exact against the oracle, so workgroups of every
+    round and on every XCD are covered."""
+    heads = np.concatenate([datagen.c1_heads(768, 51),
+                            datagen.student_t_heads(768, 52, zero_fraction=0.02)]).astype(np.float32)
+    print(f"boundary encode, heads={len(heads)}", flush=True)
+    got = codec.quantize_boundary(to_gpu(heads, device), rank=4)
+    assert (host(got[6]) == 0).all()
+    sample = list(range(0, len(heads), 97))
+    codes, s, sc, ck, cv = (host(t) for t in got[:5])
+    for h in sample:
+        e_codes, e_s, e_sc, e_ck, e_cv = oracle.quantize_kv(heads[h], 4)
+        assert codes[h].tobytes() == e_codes.tobytes(), h
+        assert s[h].tobytes() == e_s.tobytes(), h
+        assert ck[h].tobytes() == np.ascontiguousarray(e_ck).tobytes(), h
+        assert cv[h].tobytes() == np.ascontiguousarray(e_cv).tobytes(), h

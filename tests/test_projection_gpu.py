@@ -96,7 +96,7 @@ def test_decode_projection_full_config3(device):
 
 @pytest.mark.parametrize("layout", [VK, KV])
 @pytest.mark.parametrize("seqs,tokens,heads,qheads", [
-    (2, 64, 32, 32), (3, 37, 8, 4), (2, 1, 4, 4), (1, 96, 4, 2)])
+    (2, 64, 32, 32), (3, 37, 8, 4), (2, 1, 4, 4), (1, 96, 4, 2), (2, 20, 8, 2)])
 def test_chunked_projection_matches_oracle(device, layout, seqs, tokens, heads, qheads):
     print(f"chunked projection layout={layout} N={seqs} T={tokens} H={heads} Hq={qheads}",
           flush=True)
