@@ -290,8 +290,8 @@ __device__ __forceinline__ void reencode_rows(PowerShared& sh, float bs, int t, 
     s_new = newton_sqrt(mean > kBoundaryFloor ? mean : kBoundaryFloor);
     next_smoothing[row] = s_new;
   }
-  // m = cell / s_new is formed where it is used (the scale and code passes
-  // each divide again, to the same bits) rather than stored over the cells.
+  // From here on cell[] holds m = cell / s_new (the cells themselves are in the
+  // workspace already): the scale pass divides once and stores m in place.
 
   // ---- scales: max over rows of |cell / s| per column -------------------------
   // The reference keeps `value > maximum ? value : maximum` from 0 over the
@@ -304,9 +304,9 @@ __device__ __forceinline__ void reencode_rows(PowerShared& sh, float bs, int t, 
   const int wave = t >> 6;
 #pragma unroll
   for (int quarter = 0; quarter < 4; ++quarter) {
-    const auto magnitude = [&](int i) {
-      return fmaxf(fabsf(cell[32 * quarter + i] / s_new), 0.0f);
-    };
+#pragma unroll
+    for (int i = 0; i < 32; ++i) cell[32 * quarter + i] = cell[32 * quarter + i] / s_new;
+    const auto magnitude = [&](int i) { return fmaxf(fabsf(cell[32 * quarter + i]), 0.0f); };
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -328,21 +328,43 @@ __device__ __forceinline__ void reencode_rows(PowerShared& sh, float bs, int t, 
   }
   __syncthreads();  // both wavefronts' column maxima; every cell has been evaluated
   {
+    // Thread t's own slots: no other thread reads them before the barrier.
     const float maximum = fmaxf(sh.left[t], sh.right[t]);
     next_scales[t] = maximum;
-    sh.left[t] = maximum;  // thread t's own slot: no other thread reads it yet
+    sh.left[t] = maximum;
+    // The certified codes' factor RN(127 / maximum) (code_lift in codec_math.h)
+    // for a maximum of 0 or in [2^-90, 2^90]; NaN otherwise, which sends every
+    // cell of the column to the exact path below.
+    sh.right[t] = maximum == 0.0f ? 0.0f
+                  : (maximum >= 0x1p-90f && maximum <= 0x1p90f) ? kQuantizedMaximum / maximum
+                                                                : __builtin_nanf("");
   }
   __syncthreads();
 
   // ---- codes: round-half-away (:336-345), handed to the caller's sink ------
+  // The reference's q = m / maximum * 127, then trunc(q +- 0.5) clamped to
+  // +-127.  Where the lift u = fma(m, RN(127 / maximum), 0.5 + 2^-14) has a
+  // fraction of at least 2^-13, q + 0.5 lies at least 2^-15 inside
+  // (floor(u), floor(u) + 1), so the rounded q +- 0.5 truncates to floor(u)
+  // (the certificate of codec_math.h; |m| <= maximum since the maximum is
+  // over these same m).  The other cells, NaN and infinite ones among them,
+  // take the reference's expression.
   each_column([&](auto c) {
     constexpr int column = decltype(c)::value;
-    const float maximum = sh.left[column];
-    float q = maximum == 0.0f ? 0.0f : cell[column] / s_new / maximum * 127.0f;
-    q += q >= 0.0f ? 0.5f : -0.5f;
-    q = q > 127.0f ? 127.0f : q;
-    q = q < -127.0f ? -127.0f : q;
-    sink(c, static_cast<int8_t>(static_cast<int>(q)));
+    const float m = cell[column];
+    const float u = code_lift(m, sh.right[column]);
+    int code;
+    if (lift_fraction(u) >= kCodeLiftMargin) {
+      code = lifted_code(u);
+    } else {
+      const float maximum = sh.left[column];
+      float q = maximum == 0.0f ? 0.0f : m / maximum * 127.0f;
+      q += q >= 0.0f ? 0.5f : -0.5f;
+      q = q > 127.0f ? 127.0f : q;
+      q = q < -127.0f ? -127.0f : q;
+      code = static_cast<int>(q);
+    }
+    sink(c, static_cast<int8_t>(code));
     if constexpr (column % 4 == 3) __builtin_amdgcn_sched_barrier(0);
   });
 }

@@ -25,6 +25,9 @@
 //                                    random m, and m within 200 ulps of every
 //                                    tie (n + 0.5) * scale / 127.  The count of
 //                                    values left to the exact path goes to stderr.
+//   codec_math_check lift_refit      the same sweep against the refit re-encode's
+//                                    rounding, trunc(RN(q +- 0.5)) clamped to +-127
+//                                    (window_boundary.cpp:336-345)
 //   codec_math_check order           xcd_contiguous_item (work_order.h) is a
 //                                    bijection on 0 .. n-1 for every n up to
 //                                    4096 and for the bench grids
@@ -162,6 +165,11 @@ std::atomic<uint64_t> lift_fallbacks{0};
 // One lifted code against the reference expression; returns false on a
 // mismatch (a value whose lift fraction is below the margin is not a mismatch:
 // the kernel recomputes it exactly).
+// The expected code: the codec's clamp(lround(q)) or, with refit_rounding,
+// the refit re-encode's trunc(q +- 0.5) with the addition rounded to float
+// (window_boundary.cpp:336-345), q = RN(RN(m / scale) * 127) in both.
+bool refit_rounding = false;
+
 bool lift_matches(float m, float scale, float factor, uint64_t& fallbacks) {
   const float u = gdn::code_lift(m, factor);
   if (!(gdn::lift_fraction(u) >= gdn::kCodeLiftMargin)) {
@@ -169,9 +177,19 @@ bool lift_matches(float m, float scale, float factor, uint64_t& fallbacks) {
     return true;
   }
   const float scaled = scale == 0.0f ? 0.0f : m / scale * gdn::kQuantizedMaximum;
-  long expect = lroundf(scaled);
-  if (expect < -127) expect = -127;
-  if (expect > 127) expect = 127;
+  long expect;
+  if (refit_rounding) {
+    volatile float q = scaled;
+    q = q + (q >= 0.0f ? 0.5f : -0.5f);
+    float r = q;
+    r = r > 127.0f ? 127.0f : r;
+    r = r < -127.0f ? -127.0f : r;
+    expect = static_cast<long>(static_cast<int>(r));
+  } else {
+    expect = lroundf(scaled);
+    if (expect < -127) expect = -127;
+    if (expect > 127) expect = 127;
+  }
   return gdn::lifted_code(u) == expect;
 }
 
@@ -272,6 +290,9 @@ int main(int argc, char** argv) {
   } else if (strcmp(argv[1], "round") == 0) {
     check_round();
   } else if (strcmp(argv[1], "lift") == 0) {
+    check_lift();
+  } else if (strcmp(argv[1], "lift_refit") == 0) {
+    refit_rounding = true;
     check_lift();
   } else if (strcmp(argv[1], "order") == 0) {
     check_order();

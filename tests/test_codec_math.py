@@ -74,6 +74,14 @@ def test_lifted_codes_match_lround_wherever_the_margin_admits_them(checker):
     assert checked > 3_000_000_000 and failures == 0 and rc == 0
 
 
+def test_lifted_codes_match_the_refit_rounding_wherever_the_margin_admits_them(checker):
+    """The same sweep against the window-boundary re-encode's own rounding,
+    trunc(RN(q +- 0.5)) clamped to +-127 (window_boundary.cpp:336-345), which
+    the power refit and encoded_requantize now take from the lifted code."""
+    rc, checked, failures = _run(checker, "lift_refit")
+    assert checked > 3_000_000_000 and failures == 0 and rc == 0
+
+
 def test_xcd_contiguous_order_is_a_bijection(checker):
     """The streaming kernels' workgroup -> tile order (csrc/work_order.h) visits
     every tile exactly once for every grid size up to 4,096 and the bench's."""
