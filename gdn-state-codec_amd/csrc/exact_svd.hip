@@ -1,0 +1,320 @@
+// The exact-SVD boundary initializer: the reference runtime's
+// GdnStateCodecRuntime._encode_dense_boundary(dense, "exact_svd")
+// (src/gdn_state_codec/runtime.py:335-389), which takes the rank-4 truncated
+// SVD of each dense [key][value] head D with torch.linalg.svd,
+//   compensator_keys[k][r] = U[k][r] * S[r],   compensator_values[v][r] = V[v][r]
+// (r = 0..3 by decreasing singular value, stored as fp16), quantizes the fp32
+// residual D - keys * values^T and stores the codes in [value][key] order.
+//
+// The SVD here is a one-sided Jacobi (Hestenes) iteration on the provider
+// tile P = D^T ([value][key], as the runtime holds it): rotating pairs of P's
+// rows until every pair is orthogonal turns row v into u_v * s_v, so the four
+// rows of largest norm are the four left singular vectors times their singular
+// values, i.e. the compensator keys, and the matching right singular vectors
+// are D^T u = P w, normalized.  The decomposition is unique only up to the
+// signs of each (u, v) pair and, for equal singular values, the basis of
+// their subspace; the product keys * values^T, which is all the codec uses,
+// is not.  The residual then goes through the batched quant-only encode
+// (codec.hip) in the provider layout.
+//
+// One 256-thread workgroup per head.  The 128 rows live in LDS (stride 132
+// floats, so every row starts 16-byte aligned).  A sweep visits every pair of
+// rows once in 127 rounds of 64 disjoint pairs (the round-robin tournament:
+// in round r, row 127 meets row r and row (r + p) mod 127 meets
+// (r - p) mod 127 for p = 1..63); four lanes serve one pair, each holding 32
+// values of both rows.  The pair's squared norms and inner product are summed
+// in double from the fp32 rows (each product exact), the rotation follows
+// Rutishauser's formula for the smaller angle in double, and the rows are
+// rotated in fp32.  Before the sweeps the head is scaled by a power of two so
+// that its largest magnitude lies in [1/2, 1): no sum can overflow, and the
+// scaling is undone exactly on the keys.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "gdn_state_codec_kernel.h"
+#include "lane_exchange.h"
+#include "launch.h"
+#include "window_common.h"
+
+namespace gdn {
+namespace {
+
+constexpr int kSvdThreads = 256;
+constexpr int kSvdRowStride = kDim + 4;
+constexpr int kRounds = kDim - 1;          // rounds per sweep (128 rows, odd 127)
+constexpr int kSpan = kDim / 4;            // values of a row per lane
+constexpr int kMaxSweeps = 30;
+constexpr int kSvdRank = 4;
+// A pair is rotated when its cosine exceeds 2^-22; on the fp32 rows this
+// converges in 10-13 sweeps on the test heads.
+constexpr double kCosineTolerance = 0x1p-22;
+// Rows whose squared norm (after scaling) is below 2^-96 -- every value below
+// 2^-48 of the head's largest -- are taken as converged: rotating them cannot
+// change the fp32 rows of the large ones, and with subnormal values their
+// sums underflow.
+constexpr double kNegligibleSquare = 0x1p-96;
+
+// Per-head outcomes written to `status`.
+constexpr int32_t kSvdOk = 0;
+constexpr int32_t kSvdNonFiniteInput = 1;
+
+struct SvdArgs {
+  const float* provider;   // [heads][value][key]
+  float* residual;         // [heads][value][key]
+  uint16_t* keys;          // fp16 [heads][key][4]
+  uint16_t* values;        // fp16 [heads][value][4]
+  int32_t* status;         // [heads]
+};
+
+struct SvdShared {
+  float w[kDim * kSvdRowStride];  // the rows being orthogonalized
+  double norm[kDim];              // their squared norms after the sweeps
+  double y[kSvdRank][kDim];       // P w_r for the four selected rows
+  double y_norm[kSvdRank];
+  float right[kDim][kSvdRank];
+  float wave_max[kSvdThreads / 64];
+  int top[kSvdRank];
+};
+
+__device__ __forceinline__ float4 scaled(float4 v, int exponent) {
+  return make_float4(ldexpf(v.x, -exponent), ldexpf(v.y, -exponent), ldexpf(v.z, -exponent),
+                     ldexpf(v.w, -exponent));
+}
+
+__global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
+  extern __shared__ __align__(16) unsigned char dynamic[];
+  SvdShared& sh = *reinterpret_cast<SvdShared*>(dynamic);
+  const int t = threadIdx.x;
+  const uint64_t head = blockIdx.x;
+  const float* const p = a.provider + head * kTile;
+
+  // ---- load, finiteness, largest magnitude --------------------------------
+  constexpr int kLoads = kTile / 4 / kSvdThreads;  // 16 float4 per thread
+  float4 v[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) v[i] = reinterpret_cast<const float4*>(p)[i * kSvdThreads + t];
+  bool finite = true;
+  float largest = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    finite = finite && isfinite(v[i].x) && isfinite(v[i].y) && isfinite(v[i].z) &&
+             isfinite(v[i].w);
+    largest = fmaxf(largest, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
+                                   fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+  }
+  if (__syncthreads_and(finite) == 0) {  // uniform
+    if (t == 0) a.status[head] = kSvdNonFiniteInput;
+    return;
+  }
+  largest = wave_max(largest);
+  if ((t & 63) == 0) sh.wave_max[t >> 6] = largest;
+  __syncthreads();
+  largest = fmaxf(fmaxf(sh.wave_max[0], sh.wave_max[1]), fmaxf(sh.wave_max[2], sh.wave_max[3]));
+  int exponent = 0;  // largest = f * 2^exponent, f in [1/2, 1)
+  frexpf(largest, &exponent);
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int f = i * kSvdThreads + t;  // float4 index: row f / 32, column 4 (f % 32)
+    *reinterpret_cast<float4*>(sh.w + (f >> 5) * kSvdRowStride + 4 * (f & 31)) =
+        scaled(v[i], exponent);
+  }
+  __syncthreads();
+
+  // ---- Jacobi sweeps ------------------------------------------------------
+  const int pair = t >> 2;
+  const int quarter = t & 3;
+  for (int sweep = 0; sweep < kMaxSweeps; ++sweep) {
+    bool rotated = false;
+    for (int round = 0; round < kRounds; ++round) {
+      int first = kDim - 1, second = round;
+      if (pair != 0) {
+        first = round + pair;
+        if (first >= kRounds) first -= kRounds;
+        second = round - pair;
+        if (second < 0) second += kRounds;
+      }
+      float* const row_a = sh.w + first * kSvdRowStride;
+      float* const row_b = sh.w + second * kSvdRowStride;
+      float x[kSpan], y[kSpan];
+#pragma unroll
+      for (int e = 0; e < kSpan / 4; ++e) {  // float4 chunks quarter, quarter + 4, ...
+        const float4 xa = *reinterpret_cast<const float4*>(row_a + 4 * (quarter + 4 * e));
+        const float4 yb = *reinterpret_cast<const float4*>(row_b + 4 * (quarter + 4 * e));
+        x[4 * e] = xa.x, x[4 * e + 1] = xa.y, x[4 * e + 2] = xa.z, x[4 * e + 3] = xa.w;
+        y[4 * e] = yb.x, y[4 * e + 1] = yb.y, y[4 * e + 2] = yb.z, y[4 * e + 3] = yb.w;
+      }
+      double alpha = 0.0, beta = 0.0, gamma = 0.0;
+#pragma unroll
+      for (int i = 0; i < kSpan; ++i) {
+        const double xd = x[i], yd = y[i];
+        alpha = fma(xd, xd, alpha);
+        beta = fma(yd, yd, beta);
+        gamma = fma(xd, yd, gamma);
+      }
+      // The pair's four lanes add their partial sums in the same commuted
+      // order, so all four hold identical totals and take the same branch.
+      alpha += dpp_xor<1>(alpha), beta += dpp_xor<1>(beta), gamma += dpp_xor<1>(gamma);
+      alpha += dpp_xor<2>(alpha), beta += dpp_xor<2>(beta), gamma += dpp_xor<2>(gamma);
+      const bool active = alpha > kNegligibleSquare && beta > kNegligibleSquare &&
+                          gamma * gamma > kCosineTolerance * kCosineTolerance * alpha * beta;
+      if (active) {
+        // Rotate (x, y) -> (c x - s y, s x + c y) by the angle of magnitude
+        // at most pi/4 that makes the rows orthogonal: t = s/c solves
+        // t^2 + 2 zeta t - 1 = 0 with zeta = (beta - alpha) / (2 gamma).
+        const double zeta = (beta - alpha) / (2.0 * gamma);
+        const double tangent = copysign(1.0, zeta) / (fabs(zeta) + sqrt(fma(zeta, zeta, 1.0)));
+        const double cosine = 1.0 / sqrt(fma(tangent, tangent, 1.0));
+        const float c = static_cast<float>(cosine);
+        const float s = static_cast<float>(cosine * tangent);
+#pragma unroll
+        for (int i = 0; i < kSpan; ++i) {
+          const float xi = x[i], yi = y[i];
+          x[i] = fmaf(c, xi, -(s * yi));
+          y[i] = fmaf(s, xi, c * yi);
+        }
+#pragma unroll
+        for (int e = 0; e < kSpan / 4; ++e) {
+          *reinterpret_cast<float4*>(row_a + 4 * (quarter + 4 * e)) =
+              make_float4(x[4 * e], x[4 * e + 1], x[4 * e + 2], x[4 * e + 3]);
+          *reinterpret_cast<float4*>(row_b + 4 * (quarter + 4 * e)) =
+              make_float4(y[4 * e], y[4 * e + 1], y[4 * e + 2], y[4 * e + 3]);
+        }
+        rotated = true;
+      }
+      __syncthreads();
+    }
+    if (__syncthreads_or(rotated) == 0) break;  // uniform
+  }
+
+  // ---- the four rows of largest norm --------------------------------------
+  if (t < kDim) {
+    const float* const row = sh.w + t * kSvdRowStride;
+    double sum = 0.0;
+    for (int k = 0; k < kDim; ++k) {
+      const double x = row[k];
+      sum = fma(x, x, sum);
+    }
+    sh.norm[t] = sum;
+  }
+  __syncthreads();
+  if (t == 0) {
+    // Decreasing norm; equal norms in increasing row order.
+    uint64_t taken[2] = {0, 0};
+    for (int r = 0; r < kSvdRank; ++r) {
+      int best = 0;
+      double best_norm = -1.0;
+      for (int row = 0; row < kDim; ++row) {
+        const bool used = (taken[row >> 6] >> (row & 63)) & 1u;
+        if (!used && sh.norm[row] > best_norm) best_norm = sh.norm[row], best = row;
+      }
+      taken[best >> 6] |= uint64_t{1} << (best & 63);
+      sh.top[r] = best;
+    }
+  }
+  __syncthreads();
+  int top[kSvdRank];
+#pragma unroll
+  for (int r = 0; r < kSvdRank; ++r) top[r] = sh.top[r];
+
+  // ---- right vectors: y_r = P w_r (scaled P), two lanes per row -----------
+  {
+    const int row = t >> 1;
+    const int half = t & 1;
+    const float4* const source = reinterpret_cast<const float4*>(p + row * kDim + 64 * half);
+    double acc[kSvdRank] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll 4
+    for (int j = 0; j < 16; ++j) {
+      const float4 q = scaled(source[j], exponent);
+      const float qs[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = 64 * half + 4 * j + c;
+#pragma unroll
+        for (int r = 0; r < kSvdRank; ++r) {
+          acc[r] = fma(static_cast<double>(qs[c]),
+                       static_cast<double>(sh.w[top[r] * kSvdRowStride + k]), acc[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kSvdRank; ++r) {
+      acc[r] += dpp_xor<1>(acc[r]);
+      if (half == 0) sh.y[r][row] = acc[r];
+    }
+  }
+  __syncthreads();
+  if (t < kSvdRank) {
+    double sum = 0.0;
+    for (int row = 0; row < kDim; ++row) sum = fma(sh.y[t][row], sh.y[t][row], sum);
+    sh.y_norm[t] = sqrt(sum);
+  }
+  __syncthreads();
+  if (t < kDim) {
+    uint32_t bits[kSvdRank];
+#pragma unroll
+    for (int r = 0; r < kSvdRank; ++r) {
+      // A zero product (a head of rank below r + 1 whose row r is zero)
+      // leaves a zero vector; its key is zero as well.
+      const double n = sh.y_norm[r];
+      const float right = n > 0.0 ? static_cast<float>(sh.y[r][t] / n) : 0.0f;
+      sh.right[t][r] = right;
+      bits[r] = float_to_half_bits(right);
+    }
+    *reinterpret_cast<uint2*>(a.values + (head * kDim + t) * kSvdRank) =
+        make_uint2(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16));
+  }
+
+  // ---- keys and residual ----------------------------------------------------
+  const int key = t & (kDim - 1);
+  float left[kSvdRank];
+#pragma unroll
+  for (int r = 0; r < kSvdRank; ++r) left[r] = ldexpf(sh.w[top[r] * kSvdRowStride + key], exponent);
+  if (t < kDim) {
+    uint32_t bits[kSvdRank];
+#pragma unroll
+    for (int r = 0; r < kSvdRank; ++r) bits[r] = float_to_half_bits(left[r]);
+    *reinterpret_cast<uint2*>(a.keys + (head * kDim + key) * kSvdRank) =
+        make_uint2(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16));
+  }
+  __syncthreads();  // sh.right
+  float* const out = a.residual + head * kTile;
+  for (int row = t >> 7; row < kDim; row += kSvdThreads / kDim) {
+    float fit = left[0] * sh.right[row][0];
+#pragma unroll
+    for (int r = 1; r < kSvdRank; ++r) fit = fmaf(left[r], sh.right[row][r], fit);
+    out[row * kDim + key] = p[row * kDim + key] - fit;
+  }
+  if (t == 0) a.status[head] = kSvdOk;
+}
+
+}  // namespace
+}  // namespace gdn
+
+// The exact-SVD initializer for a batch of provider heads.
+extern "C" int32_t statecentric_gdn_state_codec_exact_svd_boundary_launch_v1(
+    void* stream, const float* provider, float* residual, int8_t* quantized, float* smoothing,
+    float* value_scales, uint16_t* compensator_keys, uint16_t* compensator_values,
+    int32_t* status, uint64_t heads) {
+  if (provider == nullptr || residual == nullptr || quantized == nullptr ||
+      smoothing == nullptr || value_scales == nullptr || compensator_keys == nullptr ||
+      compensator_values == nullptr || status == nullptr || heads == 0 ||
+      heads > gdn::kMaxGrid ||
+      !gdn::aligned16(provider, residual, quantized, smoothing, value_scales, compensator_keys,
+                      compensator_values, status)) {
+    return gdn::kStatusInvalidArgument;
+  }
+  const gdn::SvdArgs args{provider, residual, compensator_keys, compensator_values, status};
+  const hipError_t attribute = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(gdn::exact_svd_kernel),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(sizeof(gdn::SvdShared)));
+  if (attribute != hipSuccess) return gdn::kStatusLaunchFailed;
+  void* kernel_args[] = {const_cast<gdn::SvdArgs*>(&args)};
+  if (hipLaunchKernel(reinterpret_cast<const void*>(gdn::exact_svd_kernel),
+                      dim3(static_cast<uint32_t>(heads)), dim3(gdn::kSvdThreads), kernel_args,
+                      sizeof(gdn::SvdShared), static_cast<hipStream_t>(stream)) != hipSuccess) {
+    return gdn::kStatusLaunchFailed;
+  }
+  return statecentric_gdn_state_codec_encode_launch_v4(stream, residual, quantized, smoothing,
+                                                      value_scales, heads, gdn::kValueKey);
+}

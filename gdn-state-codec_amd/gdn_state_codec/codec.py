@@ -109,6 +109,48 @@ def quantize_boundary(dense: torch.Tensor, rank: int = 4, check: bool = True):
     return codes, smoothing, scales, keys, values, residual, status
 
 
+def exact_svd_boundary(provider: torch.Tensor, check: bool = True, residual=None):
+    """The reference runtime's ``exact_svd`` initializer
+    (``GdnStateCodecRuntime._encode_dense_boundary``,
+    ``src/gdn_state_codec/runtime.py:335-389``) for fp32 [...,128,128]
+    provider heads ([value][key], the dense state transposed): the rank-4
+    truncated SVD of each dense head by one-sided Jacobi on the GPU, then the
+    quant-only encode of the fitted residual in the provider layout.
+
+    Returns ``(codes, smoothing, scales, compensator_keys, compensator_values,
+    residual, status)``: codes int8 [...,value,key], fp16 compensators
+    [...,128,4] (keys = U*S, values = V), the fp32 residual [...,value,key]
+    (``residual`` may name the buffer to write) and int32 ``status`` per head
+    (0 ok, 1 non-finite input).  With ``check`` the call synchronizes and
+    raises ``ValueError`` for the first rejected head."""
+    heads = _tiles(provider, torch.float32, "provider state")
+    lead = tuple(provider.shape[:-2])
+    device = provider.device
+    codes = torch.empty(provider.shape, dtype=torch.int8, device=device)
+    smoothing = torch.empty(lead + (DIM,), dtype=torch.float32, device=device)
+    scales = torch.empty(lead + (DIM,), dtype=torch.float32, device=device)
+    keys = torch.empty(lead + (DIM, 4), dtype=torch.float16, device=device)
+    values = torch.empty(lead + (DIM, 4), dtype=torch.float16, device=device)
+    if residual is None:
+        residual = torch.empty(provider.shape, dtype=torch.float32, device=device)
+    _require(residual.dtype == torch.float32 and residual.is_contiguous()
+             and residual.numel() == provider.numel() and residual.device == device,
+             "GDN State Codec SVD residual must be a contiguous fp32 buffer of the "
+             "provider's size on its device")
+    status = torch.empty(lead, dtype=torch.int32, device=device)
+    _check(native().exact_svd_boundary_launch_v1(
+        _stream(), provider.data_ptr(), residual.data_ptr(), codes.data_ptr(),
+        smoothing.data_ptr(), scales.data_ptr(), keys.data_ptr(), values.data_ptr(),
+        status.data_ptr(), heads), "exact SVD boundary")
+    if check:
+        flat = status.reshape(-1).cpu()
+        bad = torch.nonzero(flat).reshape(-1)
+        if bad.numel():
+            raise ValueError(f"GDN State Codec boundary head {int(bad[0])} "
+                             f"{FIT_STATUS.get(int(flat[int(bad[0])]), 'failed')}")
+    return codes, smoothing, scales, keys, values, residual, status
+
+
 def decode(codes: torch.Tensor, smoothing: torch.Tensor, scales: torch.Tensor,
            layout: int = LAYOUT_KEY_VALUE, compensator_keys=None,
            compensator_values=None, out=None) -> torch.Tensor:

@@ -20,12 +20,14 @@ service on the gfx950 library, assembled from this package's own parts:
   cube decode backend.
 
 The interface is the reference runtime's: the method names
-(``_encode_quant_only_provider``, ``reconstruct``, ``project``, ``_slot``,
-``invalidate``, ``decode_fallback_reason``, ``fall_back_to_native``, ``step``),
-the slot buffer names, the fallback reason keys, and ``RuntimeError`` for a
-violated contract or a non-zero launch status.  vLLM configuration parsing,
-the shadow observers and the exact-SVD initializer are not part of this
-build; :class:`GdnStateCodecExperiment` carries only the fields read here.
+(``_encode_quant_only_provider``, ``_encode_dense_boundary``, ``reconstruct``,
+``project``, ``_slot``, ``invalidate``, ``decode_fallback_reason``,
+``fall_back_to_native``, ``step``), the slot buffer names, the fallback reason
+keys, the two initializers (``quant_only`` and ``exact_svd``, the latter by
+the library's Jacobi SVD kernel instead of ``torch.linalg.svd``), and
+``RuntimeError`` for a violated contract or a non-zero launch status.  vLLM
+configuration parsing and the shadow observers are not part of this build;
+:class:`GdnStateCodecExperiment` carries only the fields read here.
 """
 
 from __future__ import annotations
@@ -63,11 +65,18 @@ class GdnStateCodecExperiment:
 
     def __post_init__(self) -> None:
         self.library_dir = Path(self.library_dir)
-        if self.initializer != "quant_only":
-            raise RuntimeError("GDN State Codec on MI355X supports the quant_only initializer")
+        if self.initializer not in ("quant_only", "exact_svd"):
+            raise RuntimeError(f"gdn_state_codec.initializer {self.initializer!r} is neither "
+                               "'quant_only' nor 'exact_svd'")
         if (not isinstance(self.boundary_power_iterations, int)
+                or isinstance(self.boundary_power_iterations, bool)
                 or not 0 <= self.boundary_power_iterations <= 32):
             raise RuntimeError("gdn_state_codec.boundary_power_iterations must be in [0,32]")
+        # A fitted boundary is refitted by power iteration: the Cube refit
+        # that runs with no iterations zeroes the compensators (config.py:77-86).
+        if self.boundary_power_iterations == 0 and self.initializer != "quant_only":
+            raise RuntimeError("gdn_state_codec: the exact_svd initializer needs "
+                               "boundary_power_iterations in [1,32]")
         if self.decode_backend not in ("vector", "cube"):
             raise RuntimeError("gdn_state_codec.decode_backend must be 'vector' or 'cube'")
 
@@ -84,6 +93,8 @@ class _GdnStateCodecLibraries:
                                 "statecentric_gdn_state_codec_provider_initialize_launch_v3"),
         "encode": ("libstatecentric_gdn_state_codec_quantize_kernel.so",
                    "statecentric_gdn_state_codec_encode_launch_v4"),
+        "exact_svd_boundary": ("libstatecentric_gdn_state_codec_quantize_kernel.so",
+                               "statecentric_gdn_state_codec_exact_svd_boundary_launch_v1"),
         "decode": ("libstatecentric_gdn_state_codec_dequantize_kernel.so",
                    "statecentric_gdn_state_codec_decode_launch_v4"),
         "project_decode": ("libstatecentric_gdn_state_codec_encoded_projection_kernel.so",
@@ -314,6 +325,13 @@ class GdnStateCodecRuntime:
         return torch.cuda.current_stream().cuda_stream
 
     @property
+    def _compensated(self) -> bool:
+        """Whether the slots can carry non-zero compensators: an exact-SVD
+        boundary, or any boundary after a power-iteration refit."""
+        return (self.experiment.initializer != "quant_only"
+                or self.experiment.boundary_power_iterations > 0)
+
+    @property
     def _cube_refit(self) -> bool:
         """The quant-only refit folds the records with the Cube record GEMM, as
         the reference runtime does when no power iterations are configured."""
@@ -329,7 +347,10 @@ class GdnStateCodecRuntime:
             if not 0 <= cache_index < provider_state.shape[0]:
                 raise RuntimeError(f"GDN State Codec: cache index {cache_index} is out of range "
                                    f"for a provider state of {provider_state.shape[0]} slots")
-            slot = self._encode_quant_only_provider(provider_state[cache_index])
+            if self.experiment.initializer == "quant_only":
+                slot = self._encode_quant_only_provider(provider_state[cache_index])
+            else:
+                slot = self._encode_exact_svd_provider(provider_state[cache_index])
             if self._cube_refit:
                 self._libraries.boundary_handle(slot.heads)
             self._slots[cache_index] = slot
@@ -357,10 +378,10 @@ class GdnStateCodecRuntime:
 
     # -- boundary ------------------------------------------------------------
 
-    def _encode_quant_only_provider(self, provider_dense: torch.Tensor) -> _Slot:
-        """A new slot from one provider state [H][value][key] fp32 (device,
-        contiguous): codes, smoothing and scales of the quant-only initializer,
-        zero compensators, an empty window."""
+    @staticmethod
+    def _provider_boundary(provider_dense: torch.Tensor) -> _Generation:
+        """Checks one provider state [H][value][key] fp32 (device, contiguous)
+        and allocates the boundary generation it encodes into."""
         if provider_dense.ndim != 3:
             raise RuntimeError("GDN State Codec: the provider state must be [H,128,128] "
                                f"(value x key per head), got {tuple(provider_dense.shape)}")
@@ -370,13 +391,20 @@ class GdnStateCodecRuntime:
         if not provider_dense.is_cuda:
             raise RuntimeError("GDN State Codec: the provider state must live on the GPU")
         heads, device = provider_dense.shape[0], provider_dense.device
-        boundary = _Generation(
+        return _Generation(
             residual=torch.empty((heads, DIM, DIM), dtype=torch.int8, device=device),
             smoothing=torch.empty((heads, DIM), dtype=torch.float32, device=device),
             scales=torch.empty((heads, DIM), dtype=torch.float32, device=device),
             compensator_keys=torch.zeros((heads, DIM, RANK), dtype=torch.float16, device=device),
             compensator_values=torch.zeros((heads, DIM, RANK), dtype=torch.float16,
                                            device=device))
+
+    def _encode_quant_only_provider(self, provider_dense: torch.Tensor) -> _Slot:
+        """A new slot from one provider state [H][value][key] fp32 (device,
+        contiguous): codes, smoothing and scales of the quant-only initializer,
+        zero compensators, an empty window."""
+        boundary = self._provider_boundary(provider_dense)
+        heads = provider_dense.shape[0]
         source = provider_dense.data_ptr()
         codes, smoothing, scales = (boundary.residual.data_ptr(), boundary.smoothing.data_ptr(),
                                     boundary.scales.data_ptr())
@@ -389,22 +417,66 @@ class GdnStateCodecRuntime:
                                              heads, codec.LAYOUT_VALUE_KEY), "batched encode")
         return _Slot(boundary)
 
+    def _encode_exact_svd_provider(self, provider_dense: torch.Tensor) -> _Slot:
+        """A new slot from one provider state [H][value][key] fp32 with the
+        exact-SVD initializer (runtime.py:335-389): fp16 rank-4 compensators
+        U*S and V of each dense head's truncated SVD, and the quant-only codes
+        of the residual, by one launch of the library's Jacobi SVD.  Raises
+        for a head with a non-finite value."""
+        boundary = self._provider_boundary(provider_dense)
+        heads = provider_dense.shape[0]
+        slot = _Slot(boundary)
+        status = torch.empty((heads,), dtype=torch.int32, device=provider_dense.device)
+        _launched(self._libraries.exact_svd_boundary(
+            self._stream(), provider_dense.data_ptr(), slot.residual_workspace.data_ptr(),
+            boundary.residual.data_ptr(), boundary.smoothing.data_ptr(),
+            boundary.scales.data_ptr(), boundary.compensator_keys.data_ptr(),
+            boundary.compensator_values.data_ptr(), status.data_ptr(), heads),
+            "exact SVD initializer")
+        rejected = torch.nonzero(status.cpu()).reshape(-1)
+        if rejected.numel():
+            raise RuntimeError(f"GDN State Codec exact SVD initializer: head "
+                               f"{int(rejected[0])} holds a non-finite value")
+        return slot
+
+    def _encode_dense_boundary(self, dense: torch.Tensor,
+                               initializer: str = "exact_svd") -> _Slot:
+        """A new slot from dense [H][key][value] heads (the reference's entry,
+        runtime.py:335-389): the provider layout is their transpose."""
+        if dense.ndim != 3 or tuple(dense.shape[-2:]) != (DIM, DIM):
+            raise RuntimeError("GDN State Codec: dense boundaries must be [H,128,128] "
+                               f"(key x value per head), got {tuple(dense.shape)}")
+        provider = dense.to(torch.float32).transpose(-2, -1).contiguous()
+        if initializer == "exact_svd":
+            return self._encode_exact_svd_provider(provider)
+        if initializer == "quant_only":
+            return self._encode_quant_only_provider(provider)
+        raise RuntimeError(f"GDN State Codec: no initializer named {initializer!r}")
+
     def reconstruct(self, slot: _Slot) -> torch.Tensor:
-        """The dense [H][key][value] fp32 boundary of a quant-only slot,
-        dequantized on the GPU in the portable reference's rounding order
-        ((s * code) / 127) * scale."""
+        """The dense [H][key][value] fp32 boundary of a slot, dequantized on the
+        GPU in the portable reference's rounding order ((s * code) / 127) * scale,
+        plus the rank-4 compensator product keys * values^T when the slots can
+        carry one (the reference's reconstruct, runtime.py:550-561)."""
         dense = torch.empty((slot.heads, DIM, DIM), dtype=torch.float32,
                             device=slot.window.device)
+        keys = values = None
+        if self._compensated:  # fp16 -> fp32 widening is exact
+            keys = slot.compensator_keys.to(torch.float32)
+            values = slot.compensator_values.to(torch.float32)
         _launched(self._libraries.decode(
             self._stream(), slot.residual.data_ptr(), slot.smoothing.data_ptr(),
-            slot.scales.data_ptr(), None, None, dense.data_ptr(), slot.heads,
+            slot.scales.data_ptr(), None if keys is None else keys.data_ptr(),
+            None if values is None else values.data_ptr(), dense.data_ptr(), slot.heads,
             codec.LAYOUT_VALUE_KEY), "decode")
         return dense.transpose(-2, -1)
 
     def project(self, slot: _Slot, query: torch.Tensor,
                 query_scale: float = QWEN_QUERY_SCALE) -> torch.Tensor:
-        """The boundary readout of a slot for one decode query, [1,1,H/2,128]
-        bf16 (value head h reads query head h/2); returns [1,1,H,128] fp32."""
+        """The readout of a slot's quantized boundary residual for one decode
+        query, [1,1,H/2,128] bf16 (value head h reads query head h/2); returns
+        [1,1,H,128] fp32.  This is the encoded projection's contract: the
+        compensator term is not part of it."""
         _enforce(query, "the query", _Expect((1, 1, slot.heads // 2, DIM), torch.bfloat16),
                  slot.window.device)
         out = torch.empty((1, 1, slot.heads, DIM), dtype=torch.float32,

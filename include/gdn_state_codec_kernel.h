@@ -116,6 +116,27 @@ int32_t statecentric_gdn_state_codec_quantize_boundary_launch_v1(
     float* smoothing, float* value_scales, float* compensator_keys,
     float* compensator_values, int32_t* status, uint64_t heads, uint32_t rank);
 
+/* The runtime's exact-SVD boundary initializer for `heads` fp32 provider tiles
+ * ([value][key], the dense [key][value] state transposed), replacing
+ * GdnStateCodecRuntime._encode_dense_boundary(dense, "exact_svd")
+ * (src/gdn_state_codec/runtime.py:335-389), which calls torch.linalg.svd:
+ * the rank-4 truncated SVD of each dense head D = U S V^T by one-sided Jacobi,
+ * compensator_keys fp16 [heads][128 key][4] = U[:, r] * S[r] and
+ * compensator_values fp16 [heads][128 value][4] = V[:, r], r = 0..3 by
+ * decreasing singular value; residual fp32 [heads][value][key] = the provider
+ * tile minus the fp32 rank-4 product; then encode_launch_v4 of the residual in
+ * the [value][key] layout (quantized [value][key], smoothing by key,
+ * value_scales by value).  status[h] is 0, or 1 when head h holds a
+ * non-finite value (its outputs are then unspecified).  The signs of each
+ * (U, V) column pair are the iteration's own (an SVD fixes only their
+ * product); the fp32 rank-4 product agrees with a float64 SVD to about 1e-5 of
+ * the largest singular value.  1 <= heads <= 2^31-1.  No C-ABI counterpart in
+ * the reference. */
+int32_t statecentric_gdn_state_codec_exact_svd_boundary_launch_v1(
+    void* stream, const float* provider, float* residual, int8_t* quantized,
+    float* smoothing, float* value_scales, uint16_t* compensator_keys,
+    uint16_t* compensator_values, int32_t* status, uint64_t heads);
+
 /* Decode of `heads` tiles.  compensator_keys/values are both NULL (quant-only,
  * rank 0) or both fp32 [heads][128][4] (rank 4, the dequantize_launch_v1 form). */
 int32_t statecentric_gdn_state_codec_decode_launch_v4(

@@ -210,6 +210,19 @@ def test_quantize_boundary_admission(lib):
             assert lib.quantize_boundary_launch_v1(None, *args, 2, 0) == 1
 
 
+def test_exact_svd_boundary_admission(lib):
+    """The exact-SVD initializer: every pointer required and
+    1 <= heads <= 2^31-1; all rejected before any HIP call."""
+    p = ctypes.c_void_p(16)
+    eight = [p] * 8
+    for heads in (0, 1 << 31):
+        assert lib.exact_svd_boundary_launch_v1(None, *eight, heads) == 1
+    for i in range(8):
+        args = list(eight)
+        args[i] = None
+        assert lib.exact_svd_boundary_launch_v1(None, *args, 2) == 1
+
+
 def test_noalloc_refit_admission(lib):
     """The allocation-free refit: every pointer required, at most 512 states
     when the power refit needs the scratch workspace, 16384 without it, and
@@ -314,6 +327,7 @@ _ALIGNMENT_CASES = {
     "window_boundary_cube_finish_launch_v1": [None] + ["P"] * 15 + [2],
     "bf16_cube_matmul_launch_v1": [None, "P", "P", "P", 2, 16, 16, 1],
     "quantize_boundary_launch_v1": [None] + ["P"] * 8 + [2, 4],
+    "exact_svd_boundary_launch_v1": [None] + ["P"] * 8 + [2],
     "capsule_serialize_launch_v1": [None] + ["P"] * 9 + [1, _GEOMETRY, 1, 1, "P", "P", 1 << 20,
                                                           "P", 2],
     "capsule_restore_launch_v1": [None, "P", "P", "P", 1 << 20, _GEOMETRY, 1, 1, "P", 1]

@@ -111,23 +111,29 @@ def slot_buffers(slot) -> dict:
             "positions": h(slot.positions, np.uint32)}
 
 
-@pytest.mark.parametrize("backend,power", [("vector", 0), ("cube", 0), ("vector", 3)])
-def test_runtime_steps_through_two_window_refits(device, backend, power):
+@pytest.mark.parametrize("backend,power,initializer", [
+    ("vector", 0, "quant_only"), ("cube", 0, "quant_only"), ("vector", 3, "quant_only"),
+    ("vector", 3, "exact_svd"), ("cube", 2, "exact_svd")])
+def test_runtime_steps_through_two_window_refits(device, backend, power, initializer):
     """40 decode tokens through GdnStateCodecRuntime.step (two refits): every
     step and refit is checked against the oracle applied to the slot's own
-    buffers just before it."""
+    buffers just before it.  With the exact-SVD initializer the first window
+    runs on a boundary with fitted compensators."""
     from gdn_state_codec import GdnStateCodecExperiment
     from oracle import window as W
     import windowgen as WG
     from test_window_gpu import check_step
 
-    print(f"runtime steps backend={backend} power={power}", flush=True)
+    print(f"runtime steps backend={backend} power={power} initializer={initializer}",
+          flush=True)
     heads = 32
     runtime = GdnStateCodecRuntime(GdnStateCodecExperiment(
-        decode_backend=backend, boundary_power_iterations=power))
+        decode_backend=backend, boundary_power_iterations=power, initializer=initializer))
     provider = datagen.c1_heads(2 * heads, 9).reshape(2, heads, 128, 128)
     state = torch.from_numpy(provider).to(device)
     slot = runtime._slot(state, 1)
+    if initializer == "exact_svd":
+        assert slot.compensator_keys.abs().max().item() > 0
     try:
         for t in range(40):
             inp = WG.bf16_inputs(heads, 300 + t)
@@ -176,5 +182,42 @@ def test_runtime_steps_through_two_window_refits(device, backend, power):
                 for name in ref:
                     assert after[name].tobytes() == ref[name].tobytes(), (t, name)
         assert runtime.boundary_refits == 2
+    finally:
+        runtime.close()
+
+
+def test_exact_svd_slot_and_reconstruct(device):
+    """The exact-SVD initializer's slot holds what codec.exact_svd_boundary
+    writes for the same provider state (byte for byte), an empty window, and
+    reconstructs to the dequantized residual plus the fp16 compensator product;
+    the reference's dense entry point (_encode_dense_boundary, [key][value]
+    heads) gives the same slot."""
+    from gdn_state_codec import GdnStateCodecExperiment
+
+    heads = 16
+    print(f"runtime exact SVD slot, heads={heads}", flush=True)
+    runtime = GdnStateCodecRuntime(GdnStateCodecExperiment(
+        initializer="exact_svd", boundary_power_iterations=2))
+    provider = datagen.student_t_heads(2 * heads, 83).reshape(2, heads, 128, 128)
+    state = torch.from_numpy(provider).to(device)
+    try:
+        slot = runtime._slot(state, 0)
+        expect = codec.exact_svd_boundary(state[0].contiguous())
+        for name, want in zip(("residual", "smoothing", "scales", "compensator_keys",
+                               "compensator_values"), expect):
+            assert to_np(getattr(slot, name)).tobytes() == to_np(want).tobytes(), name
+        assert not to_np(slot.positions).any()
+        dense = runtime._encode_dense_boundary(state[0].transpose(-2, -1))
+        assert to_np(dense.residual).tobytes() == to_np(slot.residual).tobytes()
+        assert (to_np(dense.compensator_keys).tobytes()
+                == to_np(slot.compensator_keys).tobytes())
+        got = to_np(runtime.reconstruct(slot))
+        codes, s, sc = (to_np(slot.residual), to_np(slot.smoothing), to_np(slot.scales))
+        base = oracle.decode_heads(codes, s, sc, oracle.LAYOUT_VALUE_KEY).transpose(0, 2, 1)
+        keys = to_np(slot.compensator_keys).astype(np.float64)
+        values = to_np(slot.compensator_values).astype(np.float64)
+        want = base + keys @ values.transpose(0, 2, 1)
+        assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
+        assert np.abs(got - provider[0].transpose(0, 2, 1)).max() < 0.05 * np.abs(provider).max()
     finally:
         runtime.close()
