@@ -9,8 +9,9 @@ the working set.  Kernel durations come from HIP events recorded on the stream
 the kernels are launched on (torch's current stream).  The windowed decode
 step, its window-boundary refit, the encoded rank-4 chain, the capsule wire
 format (serialize / restore), the rank-4 boundary encode of the capsule
-factory, config 1 (the 32-head round trip) and config 5 (the slot-indexed fp32
-and bf16 pools) are reported beside the headline line.
+factory, the runtime's exact-SVD initializer, config 1 (the 32-head round
+trip) and config 5 (the slot-indexed fp32 and bf16 pools) are reported beside
+the headline line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-pool]
 
@@ -877,6 +878,92 @@ def bench_boundary_fit(steps: int, cpu: bool):
     return results
 
 
+def bench_exact_svd(steps: int, cpu: bool):
+    """The runtime's exact-SVD boundary initializer
+    (exact_svd_boundary_launch_v1; runtime.py:335-389) on C1-style provider
+    heads: 32 heads (one layer slot) and 8,192, timed back to back.  The Jacobi
+    sweeps are a chain of 127 rounds per sweep behind one barrier each, so the
+    time is the chain, not HBM.  The CPU baseline is the reference's own call,
+    torch.linalg.svd in fp32 on the host, over the 32-head slot plus the
+    residual and the quant stage (the oracle's encode), on the host's cores;
+    the GPU's rank-4 product is checked against the float64 SVD on it."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from gdn_state_codec import native
+    from oracle import svd as S
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(31)
+    heads = WINDOW_STATES
+    provider = _c1_style_state((heads, 128, 128), gen, dev)
+    out = {"residual": torch.empty_like(provider),
+           "codes": torch.empty((heads, 128, 128), dtype=torch.int8, device=dev),
+           "smoothing": torch.empty((heads, 128), device=dev),
+           "scales": torch.empty((heads, 128), device=dev),
+           "keys": torch.empty((heads, 128, 4), dtype=torch.float16, device=dev),
+           "values": torch.empty((heads, 128, 4), dtype=torch.float16, device=dev),
+           "status": torch.empty((heads,), dtype=torch.int32, device=dev)}
+    lib, stream = native(), torch.cuda.current_stream().cuda_stream
+    fn = lib.exact_svd_boundary_launch_v1
+
+    def call(n):
+        return (stream, provider.data_ptr(), *(out[k].data_ptr() for k in out), n)
+
+    results = {"workload": "exact-SVD initializer (rank-4 truncated SVD by Jacobi + quant "
+                           "stage) of C1-style provider heads"}
+    for n in (32, heads):
+        us = _time_back_to_back(fn, [call(n)], max(steps // 4, 2))
+        results[f"heads_{n}"] = {"ms_per_batch": us / 1e3, "heads_per_s": n / (us * 1e-6)}
+        _log(f"exact SVD: {n} heads in {us / 1e3:.3f} ms ({n / (us * 1e-6):.0f} heads/s)")
+    torch.cuda.synchronize()
+    assert int(out["status"].abs().sum()) == 0
+    sample = 32
+    x = provider[:sample].cpu().numpy()
+    residual = out["residual"][:sample].cpu().numpy()
+    top = np.empty(sample)
+    error = np.empty(sample)
+    for h in range(sample):
+        _, _, singular, product = S.svd_fit(x[h].T)
+        fit = (x[h].astype(np.float64) - residual[h]).T
+        top[h] = singular[0]
+        error[h] = np.abs(fit - product).max() / singular[0]
+    results["rank4_product_error_vs_float64_svd"] = {
+        "max_over_top_singular_value": float(error.max()), "heads_checked": sample}
+    if not cpu:
+        return results
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    dense = torch.from_numpy(x).transpose(-2, -1).contiguous()
+
+    def reference_path():
+        u, s, vt = torch.linalg.svd(dense, full_matrices=False)
+        left = u[:, :, :4] * s[:, None, :4]
+        right = vt[:, :4, :].transpose(-2, -1)
+        fitted = dense - torch.bmm(left, right.transpose(-2, -1))
+        oracle.encode_heads(fitted.transpose(-2, -1).contiguous().numpy(),
+                            oracle.LAYOUT_VALUE_KEY, threads=threads)
+
+    reference_path()
+    repeats = 0
+    t0 = time.perf_counter()
+    while repeats < 3 or (time.perf_counter() - t0 < 5.0 and repeats < 200):
+        reference_path()
+        repeats += 1
+    seconds = (time.perf_counter() - t0) / repeats
+    results["cpu_baseline"] = {
+        "value": sample / seconds, "unit": "heads/s", "cores": threads, "kind": "port",
+        "cpu_model": _cpu_model(), "seconds_per_batch": seconds,
+        "sample": f"the first {sample} heads (one slot): fp32 torch.linalg.svd, the fitted "
+                  f"residual and the quant stage, {repeats} repeats"}
+    _log(f"cpu exact SVD ({threads} threads): {sample / seconds:.1f} heads/s, "
+         f"{seconds * 1e3:.2f} ms per {sample}-head slot; GPU rank-4 product within "
+         f"{error.max():.2e} of the float64 SVD")
+    return results
+
+
 CAPSULE_GEOMETRY = "0123456789abcdef" * 4
 SHA_BLOCKS_PER_CAPSULE = lambda p: (21624 + 1536 * p + 9 + 63) // 64  # noqa: E731
 
@@ -1305,6 +1392,7 @@ def profile_pass() -> int:
     bench_capsule(1, 0)
     torch.cuda.empty_cache()
     bench_boundary_fit(1, False)
+    bench_exact_svd(1, False)
     torch.cuda.empty_cache()
     bench_pool(1, 0, "f32")
     bench_pool(1, 0, "bf16")
@@ -1393,6 +1481,7 @@ def main() -> int:
             extra["capsule"]["cpu_baseline"] = cpu_baseline_capsule()
         torch.cuda.empty_cache()
         extra["boundary_fit"] = bench_boundary_fit(args.steps, not args.no_cpu)
+        extra["exact_svd"] = bench_exact_svd(args.steps, not args.no_cpu)
         extra["config1"] = bench_config1(args.steps, not args.no_cpu)
     if not args.no_pool and not args.only_codec:
         torch.cuda.empty_cache()

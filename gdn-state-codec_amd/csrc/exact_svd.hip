@@ -17,17 +17,19 @@
 // is not.  The residual then goes through the batched quant-only encode
 // (codec.hip) in the provider layout.
 //
-// One 256-thread workgroup per head.  The 128 rows live in LDS (stride 132
-// floats, so every row starts 16-byte aligned).  A sweep visits every pair of
-// rows once in 127 rounds of 64 disjoint pairs (the round-robin tournament:
-// in round r, row 127 meets row r and row (r + p) mod 127 meets
-// (r - p) mod 127 for p = 1..63); four lanes serve one pair, each holding 32
-// values of both rows.  The pair's squared norms and inner product are summed
-// in double from the fp32 rows (each product exact), the rotation follows
-// Rutishauser's formula for the smaller angle in double, and the rows are
-// rotated in fp32.  Before the sweeps the head is scaled by a power of two so
-// that its largest magnitude lies in [1/2, 1): no sum can overflow, and the
-// scaling is undone exactly on the keys.
+// One 256-thread workgroup per head.  The 128 rows live in LDS in double
+// (stride 130, so every row starts 16-byte aligned; 130 KiB, one workgroup
+// per CU).  A sweep visits every pair of rows once in 127 rounds of 64
+// disjoint pairs (the round-robin tournament: in round r, row 127 meets row r
+// and row (r + p) mod 127 meets (r - p) mod 127 for p = 1..63); four lanes
+// serve one pair, each holding 32 values of both rows.  The rotation follows
+// Rutishauser's formula for the smaller angle.  Everything up to the outputs
+// is double: with fp32 rows the rounding of the rotations, amplified by the
+// gap between the fourth and fifth singular values (1-5% on Gaussian heads),
+// left the rank-4 product 1e-5..6e-5 of the largest singular value off; in
+// double it is the fp32 rounding of the outputs.  Before the sweeps the head
+// is scaled by a power of two so that its largest magnitude lies in [1/2, 1),
+// and the scaling is undone exactly on the keys.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -41,18 +43,17 @@ namespace gdn {
 namespace {
 
 constexpr int kSvdThreads = 256;
-constexpr int kSvdRowStride = kDim + 4;
+constexpr int kSvdRowStride = kDim + 2;  // doubles
 constexpr int kRounds = kDim - 1;          // rounds per sweep (128 rows, odd 127)
 constexpr int kSpan = kDim / 4;            // values of a row per lane
 constexpr int kMaxSweeps = 30;
 constexpr int kSvdRank = 4;
-// A pair is rotated when its cosine exceeds 2^-22; on the fp32 rows this
-// converges in 10-13 sweeps on the test heads.
-constexpr double kCosineTolerance = 0x1p-22;
+// A pair is rotated when its cosine exceeds 2^-36; this converges in 10-13
+// sweeps on the test heads.
+constexpr double kCosineTolerance = 0x1p-36;
 // Rows whose squared norm (after scaling) is below 2^-96 -- every value below
-// 2^-48 of the head's largest -- are taken as converged: rotating them cannot
-// change the fp32 rows of the large ones, and with subnormal values their
-// sums underflow.
+// 2^-48 of the head's largest -- are taken as converged: their share of any
+// singular value is below the fp32 rounding of the outputs.
 constexpr double kNegligibleSquare = 0x1p-96;
 
 // Per-head outcomes written to `status`.
@@ -68,7 +69,7 @@ struct SvdArgs {
 };
 
 struct SvdShared {
-  float w[kDim * kSvdRowStride];  // the rows being orthogonalized
+  double w[kDim * kSvdRowStride];  // the rows being orthogonalized
   double norm[kDim];              // their squared norms after the sweeps
   double y[kSvdRank][kDim];       // P w_r for the four selected rows
   double y_norm[kSvdRank];
@@ -77,9 +78,9 @@ struct SvdShared {
   int top[kSvdRank];
 };
 
-__device__ __forceinline__ float4 scaled(float4 v, int exponent) {
-  return make_float4(ldexpf(v.x, -exponent), ldexpf(v.y, -exponent), ldexpf(v.z, -exponent),
-                     ldexpf(v.w, -exponent));
+// x * 2^-exponent in double (exact for every fp32 x).
+__device__ __forceinline__ double scaled(float x, int exponent) {
+  return ldexp(static_cast<double>(x), -exponent);
 }
 
 __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
@@ -116,8 +117,11 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
 #pragma unroll
   for (int i = 0; i < kLoads; ++i) {
     const int f = i * kSvdThreads + t;  // float4 index: row f / 32, column 4 (f % 32)
-    *reinterpret_cast<float4*>(sh.w + (f >> 5) * kSvdRowStride + 4 * (f & 31)) =
-        scaled(v[i], exponent);
+    double* const to = sh.w + (f >> 5) * kSvdRowStride + 4 * (f & 31);
+    *reinterpret_cast<double2*>(to) = make_double2(scaled(v[i].x, exponent),
+                                                   scaled(v[i].y, exponent));
+    *reinterpret_cast<double2*>(to + 2) = make_double2(scaled(v[i].z, exponent),
+                                                       scaled(v[i].w, exponent));
   }
   __syncthreads();
 
@@ -134,23 +138,22 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
         second = round - pair;
         if (second < 0) second += kRounds;
       }
-      float* const row_a = sh.w + first * kSvdRowStride;
-      float* const row_b = sh.w + second * kSvdRowStride;
-      float x[kSpan], y[kSpan];
+      double* const row_a = sh.w + first * kSvdRowStride;
+      double* const row_b = sh.w + second * kSvdRowStride;
+      double x[kSpan], y[kSpan];
 #pragma unroll
-      for (int e = 0; e < kSpan / 4; ++e) {  // float4 chunks quarter, quarter + 4, ...
-        const float4 xa = *reinterpret_cast<const float4*>(row_a + 4 * (quarter + 4 * e));
-        const float4 yb = *reinterpret_cast<const float4*>(row_b + 4 * (quarter + 4 * e));
-        x[4 * e] = xa.x, x[4 * e + 1] = xa.y, x[4 * e + 2] = xa.z, x[4 * e + 3] = xa.w;
-        y[4 * e] = yb.x, y[4 * e + 1] = yb.y, y[4 * e + 2] = yb.z, y[4 * e + 3] = yb.w;
+      for (int e = 0; e < kSpan / 2; ++e) {  // double2 chunks quarter, quarter + 4, ...
+        const double2 xa = *reinterpret_cast<const double2*>(row_a + 2 * (quarter + 4 * e));
+        const double2 yb = *reinterpret_cast<const double2*>(row_b + 2 * (quarter + 4 * e));
+        x[2 * e] = xa.x, x[2 * e + 1] = xa.y;
+        y[2 * e] = yb.x, y[2 * e + 1] = yb.y;
       }
       double alpha = 0.0, beta = 0.0, gamma = 0.0;
 #pragma unroll
       for (int i = 0; i < kSpan; ++i) {
-        const double xd = x[i], yd = y[i];
-        alpha = fma(xd, xd, alpha);
-        beta = fma(yd, yd, beta);
-        gamma = fma(xd, yd, gamma);
+        alpha = fma(x[i], x[i], alpha);
+        beta = fma(y[i], y[i], beta);
+        gamma = fma(x[i], y[i], gamma);
       }
       // The pair's four lanes add their partial sums in the same commuted
       // order, so all four hold identical totals and take the same branch.
@@ -164,21 +167,20 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
         // t^2 + 2 zeta t - 1 = 0 with zeta = (beta - alpha) / (2 gamma).
         const double zeta = (beta - alpha) / (2.0 * gamma);
         const double tangent = copysign(1.0, zeta) / (fabs(zeta) + sqrt(fma(zeta, zeta, 1.0)));
-        const double cosine = 1.0 / sqrt(fma(tangent, tangent, 1.0));
-        const float c = static_cast<float>(cosine);
-        const float s = static_cast<float>(cosine * tangent);
+        const double c = 1.0 / sqrt(fma(tangent, tangent, 1.0));
+        const double s = c * tangent;
 #pragma unroll
         for (int i = 0; i < kSpan; ++i) {
-          const float xi = x[i], yi = y[i];
-          x[i] = fmaf(c, xi, -(s * yi));
-          y[i] = fmaf(s, xi, c * yi);
+          const double xi = x[i], yi = y[i];
+          x[i] = fma(c, xi, -(s * yi));
+          y[i] = fma(s, xi, c * yi);
         }
 #pragma unroll
-        for (int e = 0; e < kSpan / 4; ++e) {
-          *reinterpret_cast<float4*>(row_a + 4 * (quarter + 4 * e)) =
-              make_float4(x[4 * e], x[4 * e + 1], x[4 * e + 2], x[4 * e + 3]);
-          *reinterpret_cast<float4*>(row_b + 4 * (quarter + 4 * e)) =
-              make_float4(y[4 * e], y[4 * e + 1], y[4 * e + 2], y[4 * e + 3]);
+        for (int e = 0; e < kSpan / 2; ++e) {
+          *reinterpret_cast<double2*>(row_a + 2 * (quarter + 4 * e)) =
+              make_double2(x[2 * e], x[2 * e + 1]);
+          *reinterpret_cast<double2*>(row_b + 2 * (quarter + 4 * e)) =
+              make_double2(y[2 * e], y[2 * e + 1]);
         }
         rotated = true;
       }
@@ -189,12 +191,9 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
 
   // ---- the four rows of largest norm --------------------------------------
   if (t < kDim) {
-    const float* const row = sh.w + t * kSvdRowStride;
+    const double* const row = sh.w + t * kSvdRowStride;
     double sum = 0.0;
-    for (int k = 0; k < kDim; ++k) {
-      const double x = row[k];
-      sum = fma(x, x, sum);
-    }
+    for (int k = 0; k < kDim; ++k) sum = fma(row[k], row[k], sum);
     sh.norm[t] = sum;
   }
   __syncthreads();
@@ -225,15 +224,15 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
     double acc[kSvdRank] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll 4
     for (int j = 0; j < 16; ++j) {
-      const float4 q = scaled(source[j], exponent);
-      const float qs[4] = {q.x, q.y, q.z, q.w};
+      const float4 q = source[j];
+      const double qs[4] = {scaled(q.x, exponent), scaled(q.y, exponent),
+                            scaled(q.z, exponent), scaled(q.w, exponent)};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int k = 64 * half + 4 * j + c;
 #pragma unroll
         for (int r = 0; r < kSvdRank; ++r) {
-          acc[r] = fma(static_cast<double>(qs[c]),
-                       static_cast<double>(sh.w[top[r] * kSvdRowStride + k]), acc[r]);
+          acc[r] = fma(qs[c], sh.w[top[r] * kSvdRowStride + k], acc[r]);
         }
       }
     }
@@ -269,7 +268,9 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
   const int key = t & (kDim - 1);
   float left[kSvdRank];
 #pragma unroll
-  for (int r = 0; r < kSvdRank; ++r) left[r] = ldexpf(sh.w[top[r] * kSvdRowStride + key], exponent);
+  for (int r = 0; r < kSvdRank; ++r) {
+    left[r] = static_cast<float>(ldexp(sh.w[top[r] * kSvdRowStride + key], exponent));
+  }
   if (t < kDim) {
     uint32_t bits[kSvdRank];
 #pragma unroll

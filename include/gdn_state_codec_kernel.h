@@ -129,8 +129,9 @@ int32_t statecentric_gdn_state_codec_quantize_boundary_launch_v1(
  * value_scales by value).  status[h] is 0, or 1 when head h holds a
  * non-finite value (its outputs are then unspecified).  The signs of each
  * (U, V) column pair are the iteration's own (an SVD fixes only their
- * product); the fp32 rank-4 product agrees with a float64 SVD to about 1e-5 of
- * the largest singular value.  1 <= heads <= 2^31-1.  No C-ABI counterpart in
+ * product); the iteration runs in double, so the fp32 rank-4 product agrees
+ * with a float64 SVD to the fp32 rounding of the outputs (about 1e-7 of the
+ * largest singular value).  1 <= heads <= 2^31-1.  No C-ABI counterpart in
  * the reference. */
 int32_t statecentric_gdn_state_codec_exact_svd_boundary_launch_v1(
     void* stream, const float* provider, float* residual, int8_t* quantized,

@@ -4,8 +4,9 @@ src/gdn_state_codec/runtime.py:335-389, which calls torch.linalg.svd) through
 the C-ABI, against the float64 LAPACK SVD of oracle/svd.py.
 
 The reference's result is its library's fp32 SVD, so no bit pattern is fixed;
-the tests hold the fp32 rank-4 product to 5e-5 of the largest singular value
-(fp32 SVDs, torch's included, land at 1e-6..1e-5 on these heads), the
+the tests hold the fp32 rank-4 product to 2e-6 of the largest singular value
+(the kernel iterates in double, so only the fp32 rounding of its outputs
+remains; torch's fp32 SVD lands at 3e-7..3e-6 on Gaussian heads), the
 singular values likewise, the fp16 compensators to their own rounding of
 that product, and the codes bit-exact to the oracle's quant stage applied to
 the residual the kernel wrote."""
@@ -20,7 +21,7 @@ from gdn_state_codec import codec
 from oracle import svd as S
 
 pytestmark = pytest.mark.gpu
-FIT_TOLERANCE = 5e-5  # of the largest singular value
+FIT_TOLERANCE = 2e-6  # of the largest singular value
 
 
 def host(t):
@@ -137,7 +138,7 @@ def test_non_finite_heads_are_rejected(device):
 
 
 def test_many_heads(device):
-    """1,024 heads (two rounds of workgroups on every CU): every status 0, and
+    """1,024 heads (four rounds of one workgroup per CU): every status 0, and
     every 61st head checked against the float64 SVD."""
     dense = np.concatenate([datagen.c1_heads(512, 81), datagen.student_t_heads(512, 82)])
     print(f"exact SVD initializer, heads={len(dense)}", flush=True)
