@@ -17,12 +17,14 @@
 // is not.  The residual then goes through the batched quant-only encode
 // (codec.hip) in the provider layout.
 //
-// One 256-thread workgroup per head.  The 128 rows live in LDS in double
+// One 512-thread workgroup per head.  The 128 rows live in LDS in double
 // (stride 130, so every row starts 16-byte aligned; 130 KiB, one workgroup
 // per CU).  A sweep visits every pair of rows once in 127 rounds of 64
 // disjoint pairs (the round-robin tournament: in round r, row 127 meets row r
-// and row (r + p) mod 127 meets (r - p) mod 127 for p = 1..63); four lanes
-// serve one pair, each holding 32 values of both rows.  The rotation follows
+// and row (r + p) mod 127 meets (r - p) mod 127 for p = 1..63); eight lanes
+// serve one pair, each holding 16 values of both rows.  The time is the
+// rounds' dependent latency, not issue: two waves per SIMD and short sums
+// (two accumulators per lane) hide part of it.  The rotation follows
 // Rutishauser's formula for the smaller angle.  Everything up to the outputs
 // is double: with fp32 rows the rounding of the rotations, amplified by the
 // gap between the fourth and fifth singular values (1-5% on Gaussian heads),
@@ -42,10 +44,11 @@
 namespace gdn {
 namespace {
 
-constexpr int kSvdThreads = 256;
+constexpr int kSvdThreads = 512;
+constexpr int kLanesPerPair = 8;
 constexpr int kSvdRowStride = kDim + 2;  // doubles
 constexpr int kRounds = kDim - 1;          // rounds per sweep (128 rows, odd 127)
-constexpr int kSpan = kDim / 4;            // values of a row per lane
+constexpr int kSpan = kDim / kLanesPerPair;  // values of a row per lane
 constexpr int kMaxSweeps = 30;
 constexpr int kSvdRank = 4;
 // A pair is rotated when its cosine exceeds 2^-36; this converges in 10-13
@@ -91,7 +94,7 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
   const float* const p = a.provider + head * kTile;
 
   // ---- load, finiteness, largest magnitude --------------------------------
-  constexpr int kLoads = kTile / 4 / kSvdThreads;  // 16 float4 per thread
+  constexpr int kLoads = kTile / 4 / kSvdThreads;  // 8 float4 per thread
   float4 v[kLoads];
 #pragma unroll
   for (int i = 0; i < kLoads; ++i) v[i] = reinterpret_cast<const float4*>(p)[i * kSvdThreads + t];
@@ -111,7 +114,9 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
   largest = wave_max(largest);
   if ((t & 63) == 0) sh.wave_max[t >> 6] = largest;
   __syncthreads();
-  largest = fmaxf(fmaxf(sh.wave_max[0], sh.wave_max[1]), fmaxf(sh.wave_max[2], sh.wave_max[3]));
+  largest = sh.wave_max[0];
+#pragma unroll
+  for (int w = 1; w < kSvdThreads / 64; ++w) largest = fmaxf(largest, sh.wave_max[w]);
   int exponent = 0;  // largest = f * 2^exponent, f in [1/2, 1)
   frexpf(largest, &exponent);
 #pragma unroll
@@ -126,8 +131,8 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
   __syncthreads();
 
   // ---- Jacobi sweeps ------------------------------------------------------
-  const int pair = t >> 2;
-  const int quarter = t & 3;
+  const int pair = t / kLanesPerPair;
+  const int lane = t % kLanesPerPair;
   for (int sweep = 0; sweep < kMaxSweeps; ++sweep) {
     bool rotated = false;
     for (int round = 0; round < kRounds; ++round) {
@@ -142,23 +147,25 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
       double* const row_b = sh.w + second * kSvdRowStride;
       double x[kSpan], y[kSpan];
 #pragma unroll
-      for (int e = 0; e < kSpan / 2; ++e) {  // double2 chunks quarter, quarter + 4, ...
-        const double2 xa = *reinterpret_cast<const double2*>(row_a + 2 * (quarter + 4 * e));
-        const double2 yb = *reinterpret_cast<const double2*>(row_b + 2 * (quarter + 4 * e));
+      for (int e = 0; e < kSpan / 2; ++e) {  // double2 chunks lane, lane + 8, ...
+        const double2 xa = *reinterpret_cast<const double2*>(row_a + 2 * (lane + 8 * e));
+        const double2 yb = *reinterpret_cast<const double2*>(row_b + 2 * (lane + 8 * e));
         x[2 * e] = xa.x, x[2 * e + 1] = xa.y;
         y[2 * e] = yb.x, y[2 * e + 1] = yb.y;
       }
-      double alpha = 0.0, beta = 0.0, gamma = 0.0;
+      double a2[2] = {0.0, 0.0}, b2[2] = {0.0, 0.0}, g2[2] = {0.0, 0.0};
 #pragma unroll
       for (int i = 0; i < kSpan; ++i) {
-        alpha = fma(x[i], x[i], alpha);
-        beta = fma(y[i], y[i], beta);
-        gamma = fma(x[i], y[i], gamma);
+        a2[i & 1] = fma(x[i], x[i], a2[i & 1]);
+        b2[i & 1] = fma(y[i], y[i], b2[i & 1]);
+        g2[i & 1] = fma(x[i], y[i], g2[i & 1]);
       }
-      // The pair's four lanes add their partial sums in the same commuted
-      // order, so all four hold identical totals and take the same branch.
+      double alpha = a2[0] + a2[1], beta = b2[0] + b2[1], gamma = g2[0] + g2[1];
+      // The pair's eight lanes add their partial sums in the same commuted
+      // order, so all eight hold identical totals and take the same branch.
       alpha += dpp_xor<1>(alpha), beta += dpp_xor<1>(beta), gamma += dpp_xor<1>(gamma);
       alpha += dpp_xor<2>(alpha), beta += dpp_xor<2>(beta), gamma += dpp_xor<2>(gamma);
+      alpha += dpp_xor<4>(alpha), beta += dpp_xor<4>(beta), gamma += dpp_xor<4>(gamma);
       const bool active = alpha > kNegligibleSquare && beta > kNegligibleSquare &&
                           gamma * gamma > kCosineTolerance * kCosineTolerance * alpha * beta;
       if (active) {
@@ -177,9 +184,9 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
         }
 #pragma unroll
         for (int e = 0; e < kSpan / 2; ++e) {
-          *reinterpret_cast<double2*>(row_a + 2 * (quarter + 4 * e)) =
+          *reinterpret_cast<double2*>(row_a + 2 * (lane + 8 * e)) =
               make_double2(x[2 * e], x[2 * e + 1]);
-          *reinterpret_cast<double2*>(row_b + 2 * (quarter + 4 * e)) =
+          *reinterpret_cast<double2*>(row_b + 2 * (lane + 8 * e)) =
               make_double2(y[2 * e], y[2 * e + 1]);
         }
         rotated = true;
@@ -216,20 +223,21 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
 #pragma unroll
   for (int r = 0; r < kSvdRank; ++r) top[r] = sh.top[r];
 
-  // ---- right vectors: y_r = P w_r (scaled P), two lanes per row -----------
+  // ---- right vectors: y_r = P w_r (scaled P), four lanes per row ----------
+  static_assert(kSvdThreads == 4 * kDim, "four lanes per row");
   {
-    const int row = t >> 1;
-    const int half = t & 1;
-    const float4* const source = reinterpret_cast<const float4*>(p + row * kDim + 64 * half);
+    const int row = t >> 2;
+    const int part = t & 3;  // keys 32 part .. 32 part + 31
+    const float4* const source = reinterpret_cast<const float4*>(p + row * kDim + 32 * part);
     double acc[kSvdRank] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll 4
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < 8; ++j) {
       const float4 q = source[j];
       const double qs[4] = {scaled(q.x, exponent), scaled(q.y, exponent),
                             scaled(q.z, exponent), scaled(q.w, exponent)};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const int k = 64 * half + 4 * j + c;
+        const int k = 32 * part + 4 * j + c;
 #pragma unroll
         for (int r = 0; r < kSvdRank; ++r) {
           acc[r] = fma(qs[c], sh.w[top[r] * kSvdRowStride + k], acc[r]);
@@ -239,7 +247,8 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
 #pragma unroll
     for (int r = 0; r < kSvdRank; ++r) {
       acc[r] += dpp_xor<1>(acc[r]);
-      if (half == 0) sh.y[r][row] = acc[r];
+      acc[r] += dpp_xor<2>(acc[r]);
+      if (part == 0) sh.y[r][row] = acc[r];
     }
   }
   __syncthreads();
