@@ -710,6 +710,261 @@ def bench_encoded_rank(steps: int):
     return results
 
 
+GATE_WINDOW = 16
+GATE_PROBE_STATES = 32            # encoded_projection_probe.cpp:20 (kStates)
+GATE_CHAIN_ITERATIONS = 8         # encoded_projection_probe.cpp:465 (kPowerIterations)
+GATE_REPETITIONS = 11             # encoded_projection_probe.cpp:940-987
+
+
+def bench_compression_gate():
+    """The reference's own speed gate, "compressed cycle faster than fp32"
+    (encoded_projection_probe.cpp:905-999, windowed_gdn_runtime_probe.cpp:
+    352-388), at B = 256 x 32 heads over rotated copies and at the probe's own
+    32 states."""
+    results = {"b256": _compression_gate(WINDOW_STATES, ROTATIONS),
+               "probe_shape": _compression_gate(GATE_PROBE_STATES, 1)}
+    results["workload"] = (
+        "one window cycle per slot: 16 windowed decode steps then the boundary "
+        "update, against 16 dense fp32 GDN steps (fp32_gdn_step_launch_v1) on the same "
+        "model vectors; median of 11 repetitions alternating compressed and fp32 as the "
+        "reference's probe does, each timed between HIP events on the launch stream")
+    return results
+
+
+def _compression_gate(states: int, copies: int) -> dict:
+    """Cycles at `states` states per slot over `copies` rotated slot copies
+    (launches interleaved across copies, step t of every copy before step t+1,
+    so consecutive launches touch different states and the 256 MB MALL cannot
+    hold a slot between its steps).  Compressed cycles:
+
+    * quant_only: 16 bf16 quant-only steps, then the quant-only refit
+      (window_boundary_launch_v1, power 0);
+    * power: 16 compensated bf16 steps, then the rank-4 power refit at
+      REFIT_POWER_ITERATIONS iterations;
+    * encoded_chain: the probe's cycle, 16 fp16 windowed steps
+      (windowed_gdn_step_launch_v1), the device rank chain (per rank: the seed
+      copied in, GATE_CHAIN_ITERATIONS x (prepare_int8_vector -> int8 product ->
+      finish_encoded_projection) forward and transposed, then prepare -> product ->
+      commit_encoded_rank), then encoded_requantize.  The product is
+      int8_cube_matmul_launch_v1 at the probe's 32 states and the batched
+      int8_matmul_launch_v4 at B = 256.
+
+    Positions, fitted bases and nothing else are reset outside the timed
+    region, as the probe's restore_cycle / reset_bases do."""
+    import torch
+
+    from gdn_state_codec import codec, native
+    from gdn_state_codec.window import WindowSlot
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(19 + states)
+    lib, stream = native(), torch.cuda.current_stream().cuda_stream
+
+    def unit(shape, scale):
+        v = torch.randn(shape, generator=gen, device=dev)
+        return v / v.norm(dim=-1, keepdim=True) * scale
+
+    slots, nxt, bf16_in, f16_in, dense, bases = [], [], [], [], [], []
+    for _ in range(copies):
+        x = _c1_style_state((states, 128, 128), gen, dev)
+        slot = WindowSlot.allocate(states, dev)
+        codec.encode(x, codec.LAYOUT_VALUE_KEY, slot.residual, slot.smoothing, slot.scales)
+        for t in (slot.compensator_keys, slot.compensator_values):
+            t.copy_(torch.randn(t.shape, generator=gen, device=dev) * 0.01)
+        slots.append(slot)
+        nxt.append(WindowSlot.allocate(states, dev))
+        dense.append(x)
+        log_decay = torch.log(0.9 + 0.09 * torch.rand(states, generator=gen, device=dev))
+        bf16_in.append([log_decay,
+                        (0.2 + 0.6 * torch.rand(states, generator=gen, device=dev)
+                         ).to(torch.bfloat16),
+                        unit((states // 2, 128), 1.0).to(torch.bfloat16),
+                        unit((states // 2, 128), 1.0).to(torch.bfloat16),
+                        (0.5 * torch.randn((states, 128), generator=gen, device=dev)
+                         ).to(torch.bfloat16)])
+        f16_in.append([torch.exp(log_decay),
+                       unit((states, 128), 0.25).to(torch.float16),
+                       unit((states, 128), 1.0).to(torch.float16),
+                       unit((states, 128), 1.0).to(torch.float16),
+                       (0.5 * torch.randn((states, 128), generator=gen, device=dev)
+                        ).to(torch.float16)])
+        bases.append((torch.zeros((states, 4, 128), dtype=torch.float16, device=dev),
+                      torch.zeros((states, 4, 128), dtype=torch.float16, device=dev)))
+    out_bf16 = torch.empty((states, 128), dtype=torch.bfloat16, device=dev)
+    out_f32 = torch.empty((states, 128), dtype=torch.float32, device=dev)
+    workspace = torch.empty((states, 128, 128), dtype=torch.float32, device=dev)
+    seeds = torch.zeros((4, states, 128, 16), dtype=torch.float16, device=dev)
+    seeds[..., 0] = torch.randn((4, states, 128), generator=gen, device=dev).to(torch.float16)
+    vector = torch.empty((states, 128, 16), dtype=torch.float16, device=dev)
+    output = torch.empty_like(vector)
+    quantized = torch.empty((states, 128, 16), dtype=torch.int8, device=dev)
+    dyn = torch.empty((states, 8), dtype=torch.float32, device=dev)
+    projected = torch.empty((states, 128, 16), dtype=torch.int32, device=dev)
+    corrected = torch.empty((states, 128, 16), dtype=torch.float32, device=dev)
+    req = [torch.empty((states, 128, 128), dtype=torch.int8, device=dev),
+           torch.empty((states, 128), device=dev), torch.empty((states, 128), device=dev),
+           torch.empty((states, 128, 4), dtype=torch.float16, device=dev),
+           torch.empty((states, 128, 4), dtype=torch.float16, device=dev), workspace]
+    scratch = torch.zeros(16, dtype=torch.int32, device=dev)
+    bf16_ptr = [[t.data_ptr() for t in args] for args in bf16_in]
+    f16_ptr = [[t.data_ptr() for t in args] for args in f16_in]
+
+    def ok(status):
+        if status != 0:
+            raise RuntimeError(f"compression gate launch failed: {status}")
+
+    def operands(r):
+        s = slots[r]
+        return [s.smoothing.data_ptr(), s.scales.data_ptr(), s.compensator_keys.data_ptr(),
+                s.compensator_values.data_ptr(), s.record_decay.data_ptr(),
+                s.record_keys.data_ptr(), s.record_corrections.data_ptr()]
+
+    def product(r, vec, transpose):
+        s = slots[r]
+        axis = s.smoothing if transpose else s.scales
+        ok(lib.prepare_int8_vector_launch_v1(stream, vec.data_ptr(), axis.data_ptr(),
+                                             quantized.data_ptr(), dyn.data_ptr(), states))
+        if states <= 128:
+            ok(lib.int8_cube_matmul_launch_v1(
+                stream, s.residual.data_ptr(), quantized.data_ptr(), projected.data_ptr(),
+                states, transpose, scratch.data_ptr(), scratch.data_ptr(), (states + 1) // 2))
+        else:
+            ok(lib.int8_matmul_launch_v4(stream, s.residual.data_ptr(), quantized.data_ptr(),
+                                         projected.data_ptr(), states, transpose))
+
+    def rank_chain(r):
+        left, right = bases[r]
+        for rank in range(4):
+            vector.copy_(seeds[rank])
+            for _ in range(GATE_CHAIN_ITERATIONS):
+                for src, dst, transpose in ((vector, output, 0), (output, vector, 1)):
+                    product(r, src, transpose)
+                    ok(lib.finish_encoded_projection_launch_v1(
+                        stream, projected.data_ptr(), dyn.data_ptr(), src.data_ptr(),
+                        *operands(r), left.data_ptr(), right.data_ptr(), dst.data_ptr(),
+                        states, rank, transpose))
+            product(r, vector, 0)
+            ok(lib.commit_encoded_rank_launch_v1(
+                stream, projected.data_ptr(), dyn.data_ptr(), vector.data_ptr(), *operands(r),
+                left.data_ptr(), right.data_ptr(), corrected.data_ptr(), states, rank))
+        ok(lib.encoded_requantize_launch_v1(
+            stream, slots[r].residual.data_ptr(), *operands(r), left.data_ptr(),
+            right.data_ptr(), *(t.data_ptr() for t in req), states))
+
+    def refit(r, power):
+        n = nxt[r]
+        ok(lib.window_boundary_launch_v1(
+            stream, *slots[r].pointers(), n.residual.data_ptr(), n.smoothing.data_ptr(),
+            n.scales.data_ptr(), n.compensator_keys.data_ptr(), n.compensator_values.data_ptr(),
+            workspace.data_ptr(), states, power))
+
+    def windowed(kind):
+        fn = {"quant_only": lib.windowed_gdn_step_bf16_quant_only_launch_v1,
+              "power": lib.windowed_gdn_step_bf16_launch_v1}.get(kind)
+        for _ in range(GATE_WINDOW):
+            for r in range(copies):
+                if fn is None:
+                    ok(lib.windowed_gdn_step_launch_v1(stream, *slots[r].pointers(), *f16_ptr[r],
+                                                       out_f32.data_ptr(), states))
+                else:
+                    ok(fn(stream, *slots[r].pointers(), *bf16_ptr[r], out_bf16.data_ptr(),
+                          states))
+        for r in range(copies):
+            if kind == "quant_only":
+                refit(r, 0)
+            elif kind == "power":
+                refit(r, REFIT_POWER_ITERATIONS)
+            else:
+                rank_chain(r)
+
+    def fp32_cycle(_kind):
+        for _ in range(GATE_WINDOW):
+            for r in range(copies):
+                ok(lib.fp32_gdn_step_launch_v1(stream, dense[r].data_ptr(), *f16_ptr[r],
+                                               out_f32.data_ptr(), states))
+
+    def restore(kind):
+        for r in range(copies):
+            slots[r].positions.zero_()
+            if kind == "encoded_chain":
+                for b in bases[r]:
+                    b.zero_()
+
+    def timed(cycle, kind):
+        restore(kind)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        a.record()
+        cycle(kind)
+        b.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return a.elapsed_time(b) * 1e3 / copies, wall * 1e6 / copies
+
+    kinds = ("quant_only", "power", "encoded_chain")
+    # Warm phase: whole cycles of every kind until about WARM_MS has run.
+    t0 = time.perf_counter()
+    while True:
+        for kind in kinds:
+            timed(windowed, kind)
+        timed(fp32_cycle, "fp32")
+        if (time.perf_counter() - t0) * 1e3 >= WARM_MS:
+            break
+    samples = {kind: [] for kind in (*kinds, "fp32")}
+    for rep in range(GATE_REPETITIONS):
+        order = [*kinds, "fp32"] if rep % 2 == 0 else ["fp32", *kinds]
+        for kind in order:
+            samples[kind].append(timed(fp32_cycle if kind == "fp32" else windowed, kind))
+
+    def median(values):
+        return sorted(values)[len(values) // 2]
+
+    fp32_us = median([s[0] for s in samples["fp32"]])
+    result = {"states": states, "rotated_state_copies": copies,
+              "fp32_us_per_cycle": fp32_us,
+              "fp32_wall_us_per_cycle": median([s[1] for s in samples["fp32"]])}
+    for kind in kinds:
+        us = median([s[0] for s in samples[kind]])
+        result[kind] = {"us_per_cycle": us,
+                        "wall_us_per_cycle": median([s[1] for s in samples[kind]]),
+                        "speedup_vs_fp32": fp32_us / us,
+                        "compressed_faster_than_fp32": bool(us < fp32_us)}
+        _log(f"compression gate {states} states, {kind}: {us:.1f} us per cycle against "
+             f"{fp32_us:.1f} us fp32 ({fp32_us / us:.2f}x)")
+    result["power_refit_iterations"] = REFIT_POWER_ITERATIONS
+    result["chain_power_iterations"] = GATE_CHAIN_ITERATIONS
+    result["chain_product"] = ("int8_cube_matmul_launch_v1" if states <= 128
+                               else "int8_matmul_launch_v4")
+
+    # The windowed runtime probe's single step (windowed_gdn_runtime_probe.cpp:
+    # 282-305, 352-370): one fp16 windowed step at position 7 against one fp32
+    # step, median of 11 alternating.
+    step = {"windowed": [], "fp32": []}
+    for rep in range(GATE_REPETITIONS):
+        for kind in (("windowed", "fp32") if rep % 2 == 0 else ("fp32", "windowed")):
+            for slot in slots:
+                slot.positions[:, 0] = 7
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for r in range(copies):
+                if kind == "windowed":
+                    ok(lib.windowed_gdn_step_launch_v1(stream, *slots[r].pointers(),
+                                                       *f16_ptr[r], out_f32.data_ptr(), states))
+                else:
+                    ok(lib.fp32_gdn_step_launch_v1(stream, dense[r].data_ptr(), *f16_ptr[r],
+                                                   out_f32.data_ptr(), states))
+            b.record()
+            step[kind].append(_events_ms([(a, b)])[0] * 1e3 / copies)
+    result["single_step_position_7"] = {
+        "windowed_median_us": median(step["windowed"]), "fp32_median_us": median(step["fp32"])}
+    del slots, nxt, dense, workspace, req
+    torch.cuda.empty_cache()
+    return result
+
+
 def bench_config1(steps: int, cpu: bool):
     """Config 1, the reference's CPU-runnable case: quantize + dequantize of 32
     C1-style [key][value] heads (2 MiB in).  The GPU round trip is timed back to
@@ -1181,13 +1436,17 @@ def pool_bytes_per_direction(dtype_bytes: int) -> int:
     return (POOL_BATCH - POOL_PADDING) * POOL_LAYERS * POOL_HEADS * per_head
 
 
-def bench_pool(steps: int, warmup: int, dtype_name: str):
+def bench_pool(steps: int, warmup: int, dtype_name: str, cpu: bool = True):
     """Config 5: a [30 layers][2048 slots][32 heads][128][128] state pool in
     the provider's [value][key] layout (fp32 128.8 GB or bf16 64.4 GB),
     Student-t(3) x 0.05 entries with 2% all-zero heads, a batch of 512 random
     unique slot ids of which 26 are padding (-1).  Gather-encode (pool ->
     compact codes) and decode-scatter (codes -> pool) are timed separately,
-    each launch between its own HIP events."""
+    each launch between its own HIP events.  Every encode, warm-up included,
+    runs before the first decode, so each one reads the pool as generated;
+    the decodes then write the same values back on every launch.  A sample of
+    the gathered tiles (the first live tiles in batch order) is checked bit
+    for bit in both directions and timed on the host as the CPU baseline."""
     import torch
 
     from gdn_state_codec import codec
@@ -1218,36 +1477,162 @@ def bench_pool(steps: int, warmup: int, dtype_name: str):
     pad = torch.randperm(batch, generator=gen, device=dev)[:POOL_PADDING]
     perm[pad] = -1
     layout = codec.LAYOUT_VALUE_KEY
-    codes, s, sc = codec.pool_encode(pool, perm, layout)
+    codes = torch.empty((layers, batch, heads, 128, 128), dtype=torch.int8, device=dev)
+    s = torch.empty((layers, batch, heads, 128), dtype=torch.float32, device=dev)
+    sc = torch.empty_like(s)
+
     for _ in range(warmup):
         codec.pool_encode(pool, perm, layout, codes, s, sc)
-        codec.pool_decode(codes, s, sc, perm, pool, layout)
-    enc, dec = [], []
+    enc = []
     for _ in range(steps):
-        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
         e0.record()
         codec.pool_encode(pool, perm, layout, codes, s, sc)
         e1.record()
-        codec.pool_decode(codes, s, sc, perm, pool, layout)
-        e2.record()
         enc.append((e0, e1))
-        dec.append((e1, e2))
     enc_ms = sum(_events_ms(enc)) / steps
+    sample = _pool_sample(pool, perm, codes, s, sc) if cpu else None
+    for _ in range(warmup):
+        codec.pool_decode(codes, s, sc, perm, pool, layout)
+    dec = []
+    for _ in range(steps):
+        e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+        e0.record()
+        codec.pool_decode(codes, s, sc, perm, pool, layout)
+        e1.record()
+        dec.append((e0, e1))
     dec_ms = sum(_events_ms(dec)) / steps
     nbytes = pool_bytes_per_direction(4 if dtype_name == "f32" else 2)
-    del pool, codes, s, sc
-    torch.cuda.empty_cache()
     result = {"encode_ms": enc_ms, "decode_ms": dec_ms,
               "encode_GBps": nbytes / (enc_ms * 1e-3) / 1e9,
               "decode_GBps": nbytes / (dec_ms * 1e-3) / 1e9,
               "encode_hbm_frac": nbytes / (enc_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
               "decode_hbm_frac": nbytes / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
               "bytes_per_direction": nbytes, "pool_dtype": dtype_name, "layout": "[value][key]",
-              "valid_slots": batch - POOL_PADDING, "steps": steps}
+              "valid_slots": batch - POOL_PADDING, "steps": steps,
+              "timing": "all gather-encodes first (each reads the generated pool), then all "
+                        "decode-scatters"}
     _log(f"config 5 ({dtype_name} pool): gather-encode {enc_ms:.3f} ms "
          f"({result['encode_GBps']:.0f} GB/s), decode-scatter {dec_ms:.3f} ms "
          f"({result['decode_GBps']:.0f} GB/s)")
+    if sample is not None:
+        sample["decoded"] = _pool_sample_tiles(pool, perm, sample["count"])
+        result["cpu_baseline"], result["gpu_bit_exact_on_sample"] = cpu_baseline_pool(
+            sample, dtype_name)
+    del pool, codes, s, sc
+    torch.cuda.empty_cache()
     return result
+
+
+def _pool_sample_tiles(pool, slot_ids, count: int):
+    """The first `count` live tiles of the gathered batch, in batch order
+    (layer, batch entry, head), copied to the host: fp32 or bf16 bits."""
+    import torch
+
+    live = torch.nonzero(slot_ids >= 0).flatten()
+    slots = slot_ids[live].long()
+    per_layer = live.numel() * pool.shape[2]
+    parts = []
+    for layer in range((count + per_layer - 1) // per_layer):
+        parts.append(pool[layer].index_select(0, slots).reshape(-1, 128, 128))
+    tiles = torch.cat(parts)[:count]
+    if tiles.dtype == torch.bfloat16:
+        return tiles.view(torch.int16).cpu().numpy().view("uint16")
+    return tiles.cpu().numpy()
+
+
+def _pool_sample(pool, slot_ids, codes, smoothing, scales, count: int = 49152):
+    """Gathered source tiles and the GPU's encode of them, for the CPU
+    baseline and the parity check: `count` tiles (about 3.2 GB of fp32)."""
+    import torch
+
+    torch.cuda.synchronize()
+    live = torch.nonzero(slot_ids >= 0).flatten()
+    per_layer = live.numel() * pool.shape[2]
+    layers = (count + per_layer - 1) // per_layer
+
+    def gathered(t):
+        return torch.cat([t[layer].index_select(0, live).reshape(-1, *t.shape[3:])
+                          for layer in range(layers)])[:count].cpu().numpy()
+
+    return {"count": count, "source": _pool_sample_tiles(pool, slot_ids, count),
+            "codes": gathered(codes), "smoothing": gathered(smoothing),
+            "scales": gathered(scales)}
+
+
+def cpu_baseline_pool(sample, dtype_name: str, target_seconds: float = 4.0):
+    """The reference's CPU path for a gathered pool batch: each provider
+    [value][key] tile transposed to the codec's [key][value]
+    (adapter.cpp:21-57), QuantizeBoundary's quant stage and DequantizeBoundary
+    (state_capsule.cpp:190-251, through oracle/_ref; the C restatement where
+    _ref is absent), and the result transposed back.  bf16 tiles are widened
+    before and narrowed (round to nearest even) after, since the reference's
+    pools are fp32 (runtime.py:468-469).  Timed on one thread over a bounded
+    prefix of the sample, then on every allowed core over the whole sample;
+    the GPU's codes, smoothing, scales and decoded tiles are compared with the
+    multi-thread results bit for bit."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
+    import oracle
+
+    kind = "reference" if oracle.ref_available() else "port"
+    bf16 = dtype_name == "bf16"
+
+    def round_trip(x):
+        x = oracle.bf16_to_f32(x) if bf16 else x
+        if kind == "reference":
+            c, s, sc = oracle.ref_quantize_heads(np.ascontiguousarray(x.transpose(0, 2, 1)))
+            d = oracle.ref_dequantize_heads(c, s, sc)
+            c = np.ascontiguousarray(c.transpose(0, 2, 1))
+            d = np.ascontiguousarray(d.transpose(0, 2, 1))
+        else:
+            c, s, sc = oracle.encode_heads(x, oracle.LAYOUT_VALUE_KEY, threads=1)
+            d = oracle.decode_heads(c, s, sc, oracle.LAYOUT_VALUE_KEY, threads=1)
+        if bf16:
+            d = oracle.f32_to_bf16(d.reshape(-1)).reshape(d.shape)
+        return c, s, sc, d
+
+    def run(x, threads):
+        bounds = np.linspace(0, len(x), threads + 1).astype(int)
+        t0 = time.perf_counter()
+        if threads == 1:
+            out = round_trip(x)
+        else:
+            with ThreadPoolExecutor(threads) as workers:
+                parts = list(workers.map(round_trip, [x[lo:hi] for lo, hi in
+                                                      zip(bounds, bounds[1:]) if hi > lo]))
+            out = tuple(np.concatenate([part[i] for part in parts]) for i in range(4))
+        return time.perf_counter() - t0, out
+
+    source = sample["source"]
+    per_tile = 2 * (128 * 128 * (4 if not bf16 else 2) + 128 * 128 + 2 * 128 * 4)
+    probe, _ = run(source[:64], 1)
+    n = int(min(max(64, target_seconds / max(probe, 1e-6) * 64), len(source)))
+    seconds, _ = run(source[:n], 1)
+    single = n * per_tile / seconds / 1e9
+    threads = _cpu_threads()
+    m_seconds, (c, s, sc, d) = run(source, threads)
+    multi = len(source) * per_tile / m_seconds / 1e9
+    exact = (c.tobytes() == sample["codes"].tobytes()
+             and s.tobytes() == sample["smoothing"].tobytes()
+             and sc.tobytes() == sample["scales"].tobytes()
+             and d.tobytes() == sample["decoded"].tobytes())
+    _log(f"cpu config 5 ({dtype_name}, {kind}): {single:.3f} GB/s on 1 thread ({n} tiles), "
+         f"{multi:.3f} GB/s on {threads} threads ({len(source)} tiles); "
+         f"GPU bit-exact on the sample={exact}")
+    widen = "; bf16 widened before and narrowed after in numpy" if bf16 else ""
+    return ({"value": multi, "unit": "GB/s", "cores": threads, "kind": kind,
+             "cpu_model": _cpu_model(),
+             "sample": f"the first {len(source)} live gathered tiles in batch order (layer, "
+                       f"entry, head): [value][key] -> [key][value] transpose, quantize, "
+                       f"dequantize, transpose back, split contiguously over {threads} "
+                       f"threads{widen}",
+             "seconds": m_seconds,
+             "single_thread": {"value": single, "unit": "GB/s", "cores": 1,
+                               "sample": f"the first {n} of those tiles", "seconds": seconds}},
+            bool(exact))
 
 
 def _cpu_model() -> str:
@@ -1336,6 +1721,58 @@ def cpu_baseline(state, codes, smoothing, scales, target_seconds: float = 8.0):
             "gpu_codes_bit_exact_on_sample": bool(parity and same)}
 
 
+_SYSFS_FIELDS = ("current_memory_partition", "current_compute_partition", "pp_dpm_mclk",
+                 "pp_dpm_fclk", "pp_dpm_sclk", "pp_dpm_socclk",
+                 "power_dpm_force_performance_level", "mem_info_vram_total")
+
+
+def _box_info(with_smi: bool = True) -> dict:
+    """What the box reports about the GPU this process uses: its PCI address
+    and CU count (torch), the amdgpu sysfs partition modes and DPM clock tables
+    (the '*' marks the current level), and rocm-smi's partition and clock
+    report.  Taken before and after the config-2 timing, to correlate the
+    run-to-run spread of the dequantize with the box's state."""
+    import subprocess
+
+    import torch
+
+    info = {}
+    try:
+        props = torch.cuda.get_device_properties(0)
+        info["device"] = {"name": props.name, "arch": props.gcnArchName,
+                          "cus": props.multi_processor_count,
+                          "pci": f"{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:"
+                                 f"{props.pci_device_id:02x}"}
+        bus = f"{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:{props.pci_device_id:02x}"
+    except (AttributeError, RuntimeError):
+        bus = None
+    for card in sorted(Path("/sys/class/drm").glob("card*/device")):
+        try:
+            address = card.resolve().name  # e.g. 0000:75:00.0
+        except OSError:
+            continue
+        if bus is not None and not address.startswith(bus):
+            continue
+        fields = {}
+        for name in _SYSFS_FIELDS:
+            try:
+                fields[name] = (card / name).read_text().strip()
+            except OSError:
+                pass
+        if fields:
+            info.setdefault("sysfs", {})[address] = fields
+    if with_smi:
+        try:
+            proc = subprocess.run(["rocm-smi", "--showmemorypartition", "--showcomputepartition",
+                                   "--showclocks", "--json"], capture_output=True, text=True,
+                                  timeout=30)
+            info["rocm_smi"] = json.loads(proc.stdout) if proc.returncode == 0 else \
+                {"returncode": proc.returncode, "stderr": proc.stderr[-300:]}
+        except (OSError, ValueError, subprocess.TimeoutExpired) as error:
+            info["rocm_smi"] = {"error": str(error)[-300:]}
+    return info
+
+
 def _traffic(kernel: str):
     """HBM bytes per launch of `kernel` at config 2, from the rocprofv3
     FETCH_SIZE / WRITE_SIZE summary committed under profiles/."""
@@ -1394,8 +1831,8 @@ def profile_pass() -> int:
     bench_boundary_fit(1, False)
     bench_exact_svd(1, False)
     torch.cuda.empty_cache()
-    bench_pool(1, 0, "f32")
-    bench_pool(1, 0, "bf16")
+    bench_pool(1, 0, "f32", False)
+    bench_pool(1, 0, "bf16", False)
     torch.cuda.synchronize()
     print(json.dumps({"profile_pass": "done"}), flush=True)
     return 0
@@ -1427,8 +1864,10 @@ def main() -> int:
     torch.cuda.init()
     if args.profile:
         return profile_pass()
+    box = {"before": _box_info()}
     state, codes, smoothing, scales, dense, enc_ms, dec_ms, wall_ms = bench_codec(
         args.steps, args.warmup)
+    box["after_codec"] = _box_info(with_smi=False)
     step_ms = enc_ms + dec_ms
     value = 2 * C2_BYTES / (step_ms * 1e-3) / 1e9
     enc_gbps = C2_BYTES / (enc_ms * 1e-3) / 1e9
@@ -1483,13 +1922,15 @@ def main() -> int:
         extra["boundary_fit"] = bench_boundary_fit(args.steps, not args.no_cpu)
         extra["exact_svd"] = bench_exact_svd(args.steps, not args.no_cpu)
         extra["config1"] = bench_config1(args.steps, not args.no_cpu)
+        torch.cuda.empty_cache()
+        extra["compression_gate"] = bench_compression_gate()
     if not args.no_pool and not args.only_codec:
         torch.cuda.empty_cache()
         extra["pool_codec"] = {
             "workload": "config 5: slot-indexed pool [30][2048][32][128][128], batch 512 random "
                         "unique slot ids with 26 padding (-1), Student-t(3) x 0.05, 2% zero heads",
-            "f32": bench_pool(max(args.steps // 4, 3), 1, "f32"),
-            "bf16": bench_pool(max(args.steps // 4, 3), 1, "bf16")}
+            "f32": bench_pool(max(args.steps // 4, 3), 1, "f32", not args.no_cpu),
+            "bf16": bench_pool(max(args.steps // 4, 3), 1, "bf16", not args.no_cpu)}
     line = {
         "metric": METRIC,
         "value": value,
@@ -1513,6 +1954,7 @@ def main() -> int:
         "roofline": codec_roofline(enc_ms, dec_ms),
         "cpu_baseline": cpu,
         **extra,
+        "box": box,
     }
     print(json.dumps(line), flush=True)
     return 0

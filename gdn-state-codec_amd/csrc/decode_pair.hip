@@ -738,6 +738,17 @@ extern "C" int32_t statecentric_gdn_state_codec_int8_cube_matmul_launch_v1(
                      a, b, c, transpose_a);
 }
 
+extern "C" int32_t statecentric_gdn_state_codec_int8_matmul_launch_v4(
+    void* stream, const int8_t* a, const int8_t* b, int32_t* c, uint32_t states,
+    uint32_t transpose_a) {
+  if (!a || !b || !c || states == 0 || states > gdn::kMaxWindowStates || transpose_a > 1u ||
+      !gdn::aligned16(a, b, c)) {
+    return gdn::kStatusInvalidArgument;
+  }
+  return gdn::launch(gdn::int8_matmul_kernel, dim3(states), dim3(gdn::kThreads), stream,
+                     a, b, c, transpose_a);
+}
+
 extern "C" int32_t statecentric_gdn_state_codec_finish_decode_pair_launch_v1(
     void* stream, const int32_t* projected, const float* dynamic_scale, const float* scales,
     const uint16_t* compensator_keys, const uint16_t* compensator_values,

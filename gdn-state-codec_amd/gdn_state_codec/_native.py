@@ -58,6 +58,7 @@ SIGNATURES: dict[str, list] = {
     "statecentric_gdn_state_codec_finish_decode_pair_bf16_launch_v1": [_P] * 16 + [_U32],
     "statecentric_gdn_state_codec_int8_cube_matmul_launch_v1": [
         _P, _P, _P, _P, _U32, _U32, _P, _P, _U32],
+    "statecentric_gdn_state_codec_int8_matmul_launch_v4": [_P, _P, _P, _P, _U32, _U32],
     "statecentric_gdn_state_codec_decode_runtime_step_v1": [_P] * 17 + [_U32],
     # device rank-4 chain over an encoded boundary
     "statecentric_gdn_state_codec_finish_encoded_projection_launch_v1":

@@ -152,6 +152,16 @@ int32_t statecentric_gdn_state_codec_int8_cube_matmul_launch_v1(
     void* stream, const int8_t* a, const int8_t* b, int32_t* c, uint32_t states,
     uint32_t transpose_a, void* workspace, void* tiling, uint32_t blocks);
 
+/* The same product over any batch, 1 <= states <= 16384 (the window steps'
+ * admission), in one launch: the v1 limit of 128 states is the reference's
+ * Cube block count, not a property of the product.  No workspace or tiling.
+ * Batched counterpart of int8_cube_matmul_launch_v1 above
+ * (windowed_gdn_kernel.h:108-111), for callers that run the rank chain over a
+ * whole decode batch. */
+int32_t statecentric_gdn_state_codec_int8_matmul_launch_v4(
+    void* stream, const int8_t* a, const int8_t* b, int32_t* c, uint32_t states,
+    uint32_t transpose_a);
+
 /* ---- the reference's device rank-4 chain over an encoded boundary ----------
  * (driven by host/gdn_state_codec_encoded_projection_probe.cpp:571-677:
  * prepare_int8_vector -> int8_cube_matmul -> finish_encoded_projection, forward

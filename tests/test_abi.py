@@ -120,6 +120,11 @@ def test_windowed_entry_points_admit_like_the_reference(lib):
     assert lib.int8_cube_matmul_launch_v1(None, p, p, p, 8, 0, p, p, 3) == 1
     assert lib.int8_cube_matmul_launch_v1(None, p, p, p, 8, 2, p, p, 4) == 1
     assert lib.int8_cube_matmul_launch_v1(None, p, p, p, 8, 0, None, p, 4) == 1
+    # The batched product: 1..16384 states, transpose_a <= 1, 16-byte aligned.
+    for states, transpose in ((0, 0), (16385, 0), (8, 2)):
+        assert lib.int8_matmul_launch_v4(None, p, p, p, states, transpose) == 1
+    assert lib.int8_matmul_launch_v4(None, None, p, p, 8, 0) == 1
+    assert lib.int8_matmul_launch_v4(None, p, p, ctypes.c_void_p(20), 8, 0) == 1
 
 
 def test_decode_runtime_lifecycle(lib):

@@ -196,3 +196,34 @@ def test_rank_chain_matches_the_oracle_chain(device):
         corrected_ref.tobytes()
     out = run_requantize(d, residual_d, states, device)
     assert_requantize(out, W.encoded_requantize(ref, residual))
+
+
+@pytest.mark.parametrize("transpose", [0, 1])
+def test_batched_int8_matmul_matches_the_cube_entry_point(device, transpose):
+    """int8_matmul_launch_v4 over 300 states in one launch equals the exact
+    integer product and int8_cube_matmul_launch_v1 called on chunks of at most
+    128 states (the reference's admission), int32 for int32."""
+    states = 300
+    print(f"int8_matmul_launch_v4 states={states} transpose={transpose}", flush=True)
+    g = datagen.rng(160 + transpose)
+    a = g.integers(-127, 128, (states, 128, 128), dtype=np.int8)
+    b = g.integers(-127, 128, (states, 128, 16), dtype=np.int8)
+    lhs = a.astype(np.int64)
+    if transpose:
+        lhs = lhs.transpose(0, 2, 1)
+    want = np.matmul(lhs, b.astype(np.int64)).astype(np.int32)
+    lib = native()
+    da, db = dev(a, device), dev(b, device)
+    batched = torch.full((states, 128, 16), 0x1234, dtype=torch.int32, device=device)
+    assert lib.int8_matmul_launch_v4(stream(), da.data_ptr(), db.data_ptr(),
+                                     batched.data_ptr(), states, transpose) == 0
+    chunked = torch.full((states, 128, 16), 0x4321, dtype=torch.int32, device=device)
+    scratch = torch.zeros(16, dtype=torch.int32, device=device)
+    for lo in range(0, states, 128):
+        n = min(128, states - lo)
+        assert lib.int8_cube_matmul_launch_v1(
+            stream(), da[lo].data_ptr(), db[lo].data_ptr(), chunked[lo].data_ptr(), n,
+            transpose, scratch.data_ptr(), scratch.data_ptr(), (n + 1) // 2) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(host(batched, np.int32).reshape(want.shape), want)
+    assert torch.equal(batched, chunked)

@@ -72,20 +72,25 @@ def test_out_of_range_slot_ids_are_skipped(device):
     assert got.tobytes() == oc.tobytes()
 
 
-def test_full_config5_bf16_pool(device):
-    """BASELINE config 5 at full size, in the provider's [value][key] layout:
-    a [30][2048][32] bf16 pool (64.4 GB) of Student-t(3) * 0.05 entries with
-    2% all-zero heads, 512 unique random slot ids of which 26 are -1.  After
+@pytest.mark.parametrize("dtype_name", ["f32", "bf16"])
+def test_full_config5_pool(device, dtype_name):
+    """BASELINE config 5 at full size, in the provider's [value][key] layout
+    (the reference's slot map, runtime.py:603-625): a [30][2048][32] fp32
+    (128.8 GB) or bf16 (64.4 GB) pool of Student-t(3) * 0.05 entries with 2%
+    all-zero heads, 512 unique random slot ids of which 26 are -1.  After
     pool_encode and a pool_decode back into the same pool: codes within +-127
     and every live column reaching 127; zero heads with zero codes,
     s = sqrtf(1e-8) and scale 0; padding entries of the encoded batch
     untouched; slots outside the batch unchanged; and 96 sampled tiles
     bit-exact against the oracle in both directions."""
-    print("full config-5 bf16 pool", flush=True)
+    print(f"full config-5 {dtype_name} pool", flush=True)
+    bf16 = dtype_name == "bf16"
+    dtype = torch.bfloat16 if bf16 else torch.float32
+    bits = torch.int16 if bf16 else torch.int32
     layers, slots, heads, batch = 30, 2048, 32, 512
     gen = torch.Generator(device=device)
-    gen.manual_seed(55)
-    pool = torch.empty((layers, slots, heads, 128, 128), dtype=torch.bfloat16, device=device)
+    gen.manual_seed(55 + 2 * (not bf16))
+    pool = torch.empty((layers, slots, heads, 128, 128), dtype=dtype, device=device)
     for layer in range(layers):
         for part in range(0, slots, 256):
             shape = (256, heads, 128, 128)
@@ -94,7 +99,7 @@ def test_full_config5_bf16_pool(device):
             for _ in range(3):
                 w = torch.randn(shape, generator=gen, device=device)
                 chi.addcmul_(w, w)
-            pool[layer, part:part + 256] = (z * torch.rsqrt(chi / 3) * 0.05).to(torch.bfloat16)
+            pool[layer, part:part + 256] = (z * torch.rsqrt(chi / 3) * 0.05).to(dtype)
             del z, chi, w
     zero = torch.rand((layers, slots, heads), generator=gen, device=device) < 0.02
     pool[zero] = 0
@@ -104,7 +109,7 @@ def test_full_config5_bf16_pool(device):
     outside = torch.ones(slots, dtype=torch.bool, device=device)
     outside[ids[live].long()] = False
     outside_slots = torch.nonzero(outside).flatten()[:64]
-    before = pool[:, outside_slots].view(torch.int16).to(torch.int64).sum(dim=(2, 3, 4))
+    before = pool[:, outside_slots].view(bits).to(torch.int64).sum(dim=(2, 3, 4))
 
     codes = torch.full((layers, batch, heads, 128, 128), 0x55, dtype=torch.int8, device=device)
     s = torch.full((layers, batch, heads, 128), -1.0, dtype=torch.float32, device=device)
@@ -113,15 +118,19 @@ def test_full_config5_bf16_pool(device):
     torch.cuda.synchronize()
 
     # Sampled tiles, taken before the decode overwrites the pool.
-    g = datagen.rng(56)
+    g = datagen.rng(56 + 2 * (not bf16))
     live_entries = torch.nonzero(live).flatten().cpu().numpy()
     picks = [(int(g.integers(layers)), int(g.choice(live_entries)), int(g.integers(heads)))
              for _ in range(96)]
     slot_of = ids.cpu().numpy()
-    src = np.stack([pool[l, slot_of[b], h].view(torch.int16).cpu().numpy().view(np.uint16)
-                    for l, b, h in picks])
-    ocodes, os_, osc = oracle.encode_heads(oracle.bf16_to_f32(src).reshape(-1, 128, 128), VK,
-                                           threads=8)
+
+    def tile(l, b, h):
+        t = pool[l, slot_of[b], h]
+        return t.view(torch.int16).cpu().numpy().view(np.uint16) if bf16 else t.cpu().numpy()
+
+    src = np.stack([tile(l, b, h) for l, b, h in picks])
+    src32 = oracle.bf16_to_f32(src) if bf16 else src
+    ocodes, os_, osc = oracle.encode_heads(src32.reshape(-1, 128, 128), VK, threads=8)
     for n, (l, b, h) in enumerate(picks):
         assert codes[l, b, h].cpu().numpy().tobytes() == ocodes[n].tobytes(), (l, b, h)
         assert s[l, b, h].cpu().numpy().tobytes() == os_[n].tobytes(), (l, b, h)
@@ -145,10 +154,11 @@ def test_full_config5_bf16_pool(device):
     codec.pool_decode(codes, s, sc, ids, pool, VK)
     torch.cuda.synchronize()
     odense = oracle.decode_heads(ocodes, os_, osc, VK, threads=8)
-    expect = oracle.f32_to_bf16(odense.reshape(-1)).reshape(odense.shape)
+    if bf16:
+        odense = oracle.f32_to_bf16(odense.reshape(-1)).reshape(odense.shape)
     for n, (l, b, h) in enumerate(picks):
-        got = pool[l, slot_of[b], h].view(torch.int16).cpu().numpy().view(np.uint16)
-        assert got.tobytes() == expect[n].tobytes(), (l, b, h)
-    after = pool[:, outside_slots].view(torch.int16).to(torch.int64).sum(dim=(2, 3, 4))
+        assert tile(l, b, h).tobytes() == odense[n].tobytes(), (l, b, h)
+    after = pool[:, outside_slots].view(bits).to(torch.int64).sum(dim=(2, 3, 4))
     assert torch.equal(before, after)
     del pool, codes, s, sc
+    torch.cuda.empty_cache()
