@@ -64,6 +64,9 @@ def _events_ms(pairs) -> list[float]:
     return [start.elapsed_time(end) for start, end in pairs]
 
 
+CODEC_CLOCKS: dict = {}  # what _ClockSampler saw during the config-2 timing
+
+
 def bench_codec(steps: int, warmup: int):
     import torch
 
@@ -89,18 +92,20 @@ def bench_codec(steps: int, warmup: int):
         step()
     torch.cuda.synchronize()
     enc, dec = [], []
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-        e0.record()
-        codec.encode(state, layout, codes, smoothing, scales)
-        e1.record()
-        codec.decode(codes, smoothing, scales, layout, out=dense)
-        e2.record()
-        enc.append((e0, e1))
-        dec.append((e1, e2))
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with _ClockSampler(_device_sysfs()) as sampler:
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+            e0.record()
+            codec.encode(state, layout, codes, smoothing, scales)
+            e1.record()
+            codec.decode(codes, smoothing, scales, layout, out=dense)
+            e2.record()
+            enc.append((e0, e1))
+            dec.append((e1, e2))
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    CODEC_CLOCKS.update(sampler.summary())
     enc_ms = sum(_events_ms(enc)) / steps
     dec_ms = sum(_events_ms(dec)) / steps
     _log(f"config 2: quantize {enc_ms:.3f} ms, dequantize {dec_ms:.3f} ms")
@@ -1770,7 +1775,97 @@ def _box_info(with_smi: bool = True) -> dict:
                 {"returncode": proc.returncode, "stderr": proc.stderr[-300:]}
         except (OSError, ValueError, subprocess.TimeoutExpired) as error:
             info["rocm_smi"] = {"error": str(error)[-300:]}
+        try:
+            proc = subprocess.run(["amd-smi", "metric", "--json"], capture_output=True,
+                                  text=True, timeout=60)
+            data = json.loads(proc.stdout) if proc.returncode == 0 else None
+            if isinstance(data, dict):
+                data = data.get("gpu_data", [data])
+            keep = ("clock", "power", "temperature", "throttle", "violation", "perf")
+            info["amd_smi_metric"] = [
+                {key: value for key, value in entry.items()
+                 if key == "gpu" or any(word in key.lower() for word in keep)}
+                for entry in data if isinstance(entry, dict)] if isinstance(data, list) else \
+                {"returncode": proc.returncode, "stderr": proc.stderr[-300:]}
+        except (OSError, ValueError, subprocess.TimeoutExpired) as error:
+            info["amd_smi_metric"] = {"error": str(error)[-300:]}
     return info
+
+
+class _ClockSampler:
+    """Samples the GPU's current shader clock (the '*' level of amdgpu's
+    pp_dpm_sclk) and its hwmon frequency, power and temperature readings from
+    a host thread every ~2 ms while a timed region runs; `summary()` gives
+    min / median / max per reading.  Reads sysfs only: it does not touch the
+    GPU's queues."""
+
+    def __init__(self, device_dir):
+        import threading
+
+        self.dir = device_dir
+        self.samples: dict[str, list[float]] = {}
+        self._stop = threading.Event()
+        self._thread = threading.Thread(target=self._run, daemon=True)
+        self.hwmon = sorted(p for p in (device_dir / "hwmon").glob("hwmon*/*_input")
+                            if p.name.startswith(("freq", "power", "temp"))) \
+            if device_dir is not None else []
+        self.hwmon += sorted(p for p in (device_dir / "hwmon").glob("hwmon*/power*_average")) \
+            if device_dir is not None else []
+
+    def _read(self):
+        try:
+            for line in (self.dir / "pp_dpm_sclk").read_text().splitlines():
+                if line.endswith("*"):
+                    mhz = float(line.split(":")[1].strip().rstrip("*").strip().rstrip("Mhz"))
+                    self.samples.setdefault("sclk_MHz", []).append(mhz)
+        except (OSError, ValueError, IndexError):
+            pass
+        for path in self.hwmon:
+            try:
+                self.samples.setdefault(path.name, []).append(float(path.read_text()))
+            except (OSError, ValueError):
+                pass
+
+    def _run(self):
+        while not self._stop.is_set():
+            self._read()
+            self._stop.wait(0.002)
+
+    def __enter__(self):
+        if self.dir is not None:
+            self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self.dir is not None:
+            self._thread.join()
+
+    def summary(self) -> dict:
+        out = {}
+        for name, values in self.samples.items():
+            values = sorted(values)
+            out[name] = {"min": values[0], "median": values[len(values) // 2],
+                         "max": values[-1], "samples": len(values)}
+        return out
+
+
+def _device_sysfs():
+    """The amdgpu sysfs directory of the GPU this process uses, or None."""
+    import torch
+
+    try:
+        props = torch.cuda.get_device_properties(0)
+        bus = f"{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:{props.pci_device_id:02x}"
+    except (AttributeError, RuntimeError):
+        return None
+    for card in sorted(Path("/sys/class/drm").glob("card*/device")):
+        try:
+            if card.resolve().name.startswith(bus):
+                return card
+        except OSError:
+            continue
+    return None
 
 
 def _traffic(kernel: str):
@@ -1810,9 +1905,10 @@ def _expand_probe_fraction(probe, dec_gbps: float) -> dict:
     return {"expand_probe_GBps": ceiling, "frac_of_expand_probe": dec_gbps / ceiling}
 
 
-def profile_pass() -> int:
+def profile_pass(codec_only: bool = False) -> int:
     """Two launches of each kernel at the benchmark shapes, and of the 4 GiB
-    copy probe (the known-size reference for FETCH_SIZE / WRITE_SIZE)."""
+    copy probe (the known-size reference for FETCH_SIZE / WRITE_SIZE);
+    `codec_only` stops after the config-2 codec and the probes."""
     import torch
 
     global WARM_LAUNCHES, TIMED_LAUNCHES
@@ -1820,6 +1916,10 @@ def profile_pass() -> int:
     bench_codec(2, 0)
     torch.cuda.empty_cache()
     bench_hbm_probe(repeats=2)
+    if codec_only:
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_pass": "codec"}), flush=True)
+        return 0
     bench_valu_probe(repeats=1)
     bench_decode_projection(1, 0)
     bench_chunked_projection(1, 0)
@@ -1849,6 +1949,8 @@ def main() -> int:
     parser.add_argument("--only-codec", action="store_true", help="config 2 only")
     parser.add_argument("--profile", action="store_true",
                         help="a few launches of every kernel, for rocprofv3 counter passes")
+    parser.add_argument("--profile-codec", action="store_true",
+                        help="the --profile launches of the config-2 codec and the probes only")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every head "
@@ -1862,12 +1964,14 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     torch.cuda.init()
-    if args.profile:
-        return profile_pass()
+    if args.profile or args.profile_codec:
+        return profile_pass(codec_only=args.profile_codec)
     box = {"before": _box_info()}
     state, codes, smoothing, scales, dense, enc_ms, dec_ms, wall_ms = bench_codec(
         args.steps, args.warmup)
     box["after_codec"] = _box_info(with_smi=False)
+    box["during_codec"] = dict(CODEC_CLOCKS)
+    _log(f"config 2 clocks and sensors: {json.dumps(CODEC_CLOCKS)}")
     step_ms = enc_ms + dec_ms
     value = 2 * C2_BYTES / (step_ms * 1e-3) / 1e9
     enc_gbps = C2_BYTES / (enc_ms * 1e-3) / 1e9

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "bf16_operands.h"
 #include "lane_exchange.h"
 
 namespace {
@@ -54,3 +55,25 @@ extern "C" int32_t gdn_lane_probe(void* stream, const float* in, float* out) {
 }
 
 extern "C" uint32_t gdn_lane_probe_outputs() { return kOutputs; }
+
+namespace {
+
+__global__ __launch_bounds__(256) void split_probe_kernel(const float* in, uint32_t* hi,
+                                                          uint32_t* lo, uint32_t pairs) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= pairs) return;
+  gdn::split2_pair(in[2 * i], in[2 * i + 1], hi[i], lo[i]);
+}
+
+}  // namespace
+
+// Self-check of the chunked projection's bf16 split (bf16_operands.h): in
+// holds 2 * pairs floats; hi and lo receive one packed bf16 pair per input
+// pair (low element first).
+extern "C" int32_t gdn_split_probe(void* stream, const float* in, uint32_t* hi, uint32_t* lo,
+                                   uint32_t pairs) {
+  if (in == nullptr || hi == nullptr || lo == nullptr || pairs == 0) return 1;
+  hipLaunchKernelGGL(split_probe_kernel, dim3((pairs + 255u) / 256u), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), in, hi, lo, pairs);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}

@@ -22,15 +22,23 @@ __device__ __forceinline__ uint32_t upper_halves(uint32_t first, uint32_t second
 }
 
 // Two-way bf16 split of a pair of fp32 values, rounding to nearest even
-// (one v_cvt_pk_bf16_f32 per part): hi = RN(w), lo = RN(w - hi), where
-// w - hi is exact in fp32.  |w - hi| <= 2^-8 |w| and |w - hi - lo| <= 2^-8
-// |w - hi| <= 2^-16 |w| (bf16 has 8 significant bits and fp32's exponent range,
-// so neither rounding underflows for |w| >= 2^-110).
+// (one v_cvt_pk_bf16_f32 per part): hi = RN(c), c = w clamped to the largest
+// finite bf16 (0x1.fep127), and lo = RN(w - hi), where w - hi is exact in
+// fp32 (below the clamp hi is within 2^-8 |w| of w; above it w and hi are in
+// [2^127, 2^128) and Sterbenz's lemma applies).  |w - hi| <= 2^-8 |w| and
+// |w - hi - lo| <= 2^-8 |w - hi| <= 2^-16 |w| for every finite w with
+// |w| >= 2^-110 (bf16 has 8 significant bits and fp32's exponent range, so
+// neither rounding underflows there).  Without the clamp a finite
+// |w| > 0x1.fep127 would round hi to inf and leave lo = -inf.  A NaN w gives
+// a NaN lo.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+constexpr float kLargestBf16 = 0x1.fep127f;
 
 __device__ __forceinline__ void split2_pair(float w0, float w1, uint32_t& hi, uint32_t& lo) {
-  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){w0, w1}, bf16x2_t));
+  const float c0 = fminf(fmaxf(w0, -kLargestBf16), kLargestBf16);
+  const float c1 = fminf(fmaxf(w1, -kLargestBf16), kLargestBf16);
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){c0, c1}, bf16x2_t));
   const float r0 = w0 - __uint_as_float(hi << 16);
   const float r1 = w1 - __uint_as_float(hi & 0xFFFF0000u);
   lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){r0, r1}, bf16x2_t));

@@ -619,7 +619,7 @@ __device__ __forceinline__ void decode_rows(const int8_t* tile,
       const float a = s_shared[key] * code;
       float d;
       if constexpr (kFast) {
-        d = div_by_reciprocal(a, kQuantizedMaximum, kInvQuantizedMaximum);
+        d = div_by_127(a);
       } else {
         d = a / kQuantizedMaximum;
       }
@@ -661,8 +661,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   if (t < kDim) {
     const float s = smoothing[item * kDim + t];
     s_shared[t] = s;
-    // Markstein division by 127 is exact for s * code when s is in
-    // [2^-90, 2^100] (so the product is +0 or at least 2^-90 in magnitude).
+    // The two-part division by 127 (div_by_127) is exact for s * code when s
+    // is in [2^-90, 2^100]: the product is +-0 or between 2^-90 and 2^107 in
+    // magnitude, so its low part a * 2^-35 stays a normal float.
     ok = s >= 0x1p-90f && s <= 0x1p100f;
   } else {
     scale_shared[t - kDim] = scales[item * kDim + (t - kDim)];

@@ -51,6 +51,24 @@ GDN_HD int round_half_away_small(float x) {
 constexpr float kQuantizedMaximum = 127.0f;
 constexpr float kInvQuantizedMaximum = 1.0f / 127.0f;
 
+// a / 127 from a two-part reciprocal in two operations: q = RN(a*R + RN(a*L))
+// with R = RN(1/127) and L = RN(1/127 - R) (about 2^-35), one multiply and one
+// fma.  a*(R + L) is within 2^-55 |a| of a/127 and RN(a*L) adds at most
+// 2^-24 |a*L| < 2^-58 |a|, so the fma's argument is within 2^-54 |a| (about
+// 2^-47 of the quotient) of a/127.  A quotient a/127 of a normal a is never
+// exactly halfway between two floats (that would need 127 to divide a's
+// significand, and then the quotient is representable), and it lies at least
+// 2^-31 of itself away from every halfway point, since both are multiples of
+// 2^(e-8) for a = A * 2^e; so the fma rounds to RN(a/127).  Checked for every
+// float with 2^-100 <= |a| < 2^121 by tests/test_codec_math.py; a = +-0
+// gives +-0 as IEEE division does.
+constexpr float kInvQuantizedMaximumLow =
+    static_cast<float>(1.0 / 127.0 - static_cast<double>(1.0f / 127.0f));
+
+GDN_HD float div_by_127(float a) {
+  return fmaf(a, kInvQuantizedMaximum, a * kInvQuantizedMaximumLow);
+}
+
 // The quant stage's code clamp(lround(p), -127, 127) with p = RN(RN(m / scale)
 // * 127) (state_capsule.cpp:213-219), from one fma, a fraction and a floor per
 // value.  Preconditions:

@@ -62,6 +62,7 @@ constexpr double kNegligibleSquare = 0x1p-96;
 // Per-head outcomes written to `status`.
 constexpr int32_t kSvdOk = 0;
 constexpr int32_t kSvdNonFiniteInput = 1;
+constexpr int32_t kSvdNotConverged = 2;  // a rotation still happened in the last sweep
 
 struct SvdArgs {
   const float* provider;   // [heads][value][key]
@@ -69,6 +70,7 @@ struct SvdArgs {
   uint16_t* keys;          // fp16 [heads][key][4]
   uint16_t* values;        // fp16 [heads][value][4]
   int32_t* status;         // [heads]
+  int max_sweeps;          // 1..kMaxSweeps
 };
 
 struct SvdShared {
@@ -133,7 +135,8 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
   // ---- Jacobi sweeps ------------------------------------------------------
   const int pair = t / kLanesPerPair;
   const int lane = t % kLanesPerPair;
-  for (int sweep = 0; sweep < kMaxSweeps; ++sweep) {
+  bool converged = false;
+  for (int sweep = 0; sweep < a.max_sweeps; ++sweep) {
     bool rotated = false;
     for (int round = 0; round < kRounds; ++round) {
       int first = kDim - 1, second = round;
@@ -193,7 +196,10 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
       }
       __syncthreads();
     }
-    if (__syncthreads_or(rotated) == 0) break;  // uniform
+    if (__syncthreads_or(rotated) == 0) {  // uniform
+      converged = true;
+      break;
+    }
   }
 
   // ---- the four rows of largest norm --------------------------------------
@@ -295,7 +301,42 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
     for (int r = 1; r < kSvdRank; ++r) fit = fmaf(left[r], sh.right[row][r], fit);
     out[row * kDim + key] = p[row * kDim + key] - fit;
   }
-  if (t == 0) a.status[head] = kSvdOk;
+  // An unconverged head still gets the fit of its last sweep, flagged.
+  if (t == 0) a.status[head] = converged ? kSvdOk : kSvdNotConverged;
+}
+
+}  // namespace
+}  // namespace gdn
+
+namespace gdn {
+namespace {
+
+int32_t launch_exact_svd(void* stream, const float* provider, float* residual,
+                         int8_t* quantized, float* smoothing, float* value_scales,
+                         uint16_t* compensator_keys, uint16_t* compensator_values,
+                         int32_t* status, uint64_t heads, uint32_t max_sweeps) {
+  if (provider == nullptr || residual == nullptr || quantized == nullptr ||
+      smoothing == nullptr || value_scales == nullptr || compensator_keys == nullptr ||
+      compensator_values == nullptr || status == nullptr || heads == 0 || heads > kMaxGrid ||
+      max_sweeps == 0 || max_sweeps > static_cast<uint32_t>(kMaxSweeps) ||
+      !aligned16(provider, residual, quantized, smoothing, value_scales, compensator_keys,
+                 compensator_values, status)) {
+    return kStatusInvalidArgument;
+  }
+  const SvdArgs args{provider, residual, compensator_keys, compensator_values, status,
+                     static_cast<int>(max_sweeps)};
+  const hipError_t attribute = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(exact_svd_kernel),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(sizeof(SvdShared)));
+  if (attribute != hipSuccess) return kStatusLaunchFailed;
+  void* kernel_args[] = {const_cast<SvdArgs*>(&args)};
+  if (hipLaunchKernel(reinterpret_cast<const void*>(exact_svd_kernel),
+                      dim3(static_cast<uint32_t>(heads)), dim3(kSvdThreads), kernel_args,
+                      sizeof(SvdShared), static_cast<hipStream_t>(stream)) != hipSuccess) {
+    return kStatusLaunchFailed;
+  }
+  return statecentric_gdn_state_codec_encode_launch_v4(stream, residual, quantized, smoothing,
+                                                      value_scales, heads, kValueKey);
 }
 
 }  // namespace
@@ -306,25 +347,16 @@ extern "C" int32_t statecentric_gdn_state_codec_exact_svd_boundary_launch_v1(
     void* stream, const float* provider, float* residual, int8_t* quantized, float* smoothing,
     float* value_scales, uint16_t* compensator_keys, uint16_t* compensator_values,
     int32_t* status, uint64_t heads) {
-  if (provider == nullptr || residual == nullptr || quantized == nullptr ||
-      smoothing == nullptr || value_scales == nullptr || compensator_keys == nullptr ||
-      compensator_values == nullptr || status == nullptr || heads == 0 ||
-      heads > gdn::kMaxGrid ||
-      !gdn::aligned16(provider, residual, quantized, smoothing, value_scales, compensator_keys,
-                      compensator_values, status)) {
-    return gdn::kStatusInvalidArgument;
-  }
-  const gdn::SvdArgs args{provider, residual, compensator_keys, compensator_values, status};
-  const hipError_t attribute = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(gdn::exact_svd_kernel),
-      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(sizeof(gdn::SvdShared)));
-  if (attribute != hipSuccess) return gdn::kStatusLaunchFailed;
-  void* kernel_args[] = {const_cast<gdn::SvdArgs*>(&args)};
-  if (hipLaunchKernel(reinterpret_cast<const void*>(gdn::exact_svd_kernel),
-                      dim3(static_cast<uint32_t>(heads)), dim3(gdn::kSvdThreads), kernel_args,
-                      sizeof(gdn::SvdShared), static_cast<hipStream_t>(stream)) != hipSuccess) {
-    return gdn::kStatusLaunchFailed;
-  }
-  return statecentric_gdn_state_codec_encode_launch_v4(stream, residual, quantized, smoothing,
-                                                      value_scales, heads, gdn::kValueKey);
+  return gdn::launch_exact_svd(stream, provider, residual, quantized, smoothing, value_scales,
+                               compensator_keys, compensator_values, status, heads,
+                               gdn::kMaxSweeps);
+}
+
+// The same with a caller-chosen sweep limit.
+extern "C" int32_t statecentric_gdn_state_codec_exact_svd_boundary_sweeps_launch_v1(
+    void* stream, const float* provider, float* residual, int8_t* quantized, float* smoothing,
+    float* value_scales, uint16_t* compensator_keys, uint16_t* compensator_values,
+    int32_t* status, uint64_t heads, uint32_t max_sweeps) {
+  return gdn::launch_exact_svd(stream, provider, residual, quantized, smoothing, value_scales,
+                               compensator_keys, compensator_values, status, heads, max_sweeps);
 }

@@ -18,8 +18,10 @@
 // Chunked (T queries per tile) is a [T x 128] x [128 x 128] contraction per
 // tile on bf16 MFMA (v_mfma_f32_16x16x32_bf16).  Codes are exact in bf16; the
 // fp32 operand w[t][k] = s[k] * x_t[k] is split into two bf16 parts
-// w ~ hi + lo (each rounded to nearest, remainder below 2^-16 |w|), staged in
-// LDS in the MFMA operand order.  The products with the codes are exact, so
+// w ~ hi + lo (each rounded to nearest, remainder below 2^-16 |w| for every
+// finite |w| >= 2^-110: hi is clamped to the largest finite bf16, so the top
+// of fp32's range splits into finite parts), staged in LDS in the MFMA
+// operand order.  The products with the codes are exact, so
 // the result differs from the exact readout by at most 2^-16 of sum |terms|
 // from the split plus the fp32 accumulation of 256 products (at most
 // 256 * 2^-24 of sum |terms|) and the epilogue's rounding: within

@@ -37,6 +37,7 @@ SIGNATURES: dict[str, list] = {
     "statecentric_gdn_state_codec_decode_launch_v4": [_P, _P, _P, _P, _P, _P, _P, _U64, _U32],
     "statecentric_gdn_state_codec_quantize_boundary_launch_v1": [_P] * 9 + [_U64, _U32],
     "statecentric_gdn_state_codec_exact_svd_boundary_launch_v1": [_P] * 9 + [_U64],
+    "statecentric_gdn_state_codec_exact_svd_boundary_sweeps_launch_v1": [_P] * 9 + [_U64, _U32],
     "statecentric_gdn_state_codec_pool_encode_launch_v4": [
         _P, _P, _U32, _P, _U32, _U32, _U32, _U32, _U32, _P, _P, _P],
     "statecentric_gdn_state_codec_pool_decode_launch_v4": [

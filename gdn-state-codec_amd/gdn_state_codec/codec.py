@@ -69,6 +69,8 @@ def encode(state: torch.Tensor, layout: int = LAYOUT_KEY_VALUE, codes=None,
 
 
 FIT_STATUS = {1: "holds a non-finite value", 2: "has a non-finite compensator fit"}
+SVD_STATUS = {1: "holds a non-finite value",
+              2: "did not converge within the Jacobi sweep limit"}
 
 
 def quantize_boundary(dense: torch.Tensor, rank: int = 4, check: bool = True):
@@ -109,7 +111,8 @@ def quantize_boundary(dense: torch.Tensor, rank: int = 4, check: bool = True):
     return codes, smoothing, scales, keys, values, residual, status
 
 
-def exact_svd_boundary(provider: torch.Tensor, check: bool = True, residual=None):
+def exact_svd_boundary(provider: torch.Tensor, check: bool = True, residual=None,
+                       max_sweeps: int | None = None):
     """The reference runtime's ``exact_svd`` initializer
     (``GdnStateCodecRuntime._encode_dense_boundary``,
     ``src/gdn_state_codec/runtime.py:335-389``) for fp32 [...,128,128]
@@ -121,8 +124,9 @@ def exact_svd_boundary(provider: torch.Tensor, check: bool = True, residual=None
     residual, status)``: codes int8 [...,value,key], fp16 compensators
     [...,128,4] (keys = U*S, values = V), the fp32 residual [...,value,key]
     (``residual`` may name the buffer to write) and int32 ``status`` per head
-    (0 ok, 1 non-finite input).  With ``check`` the call synchronizes and
-    raises ``ValueError`` for the first rejected head."""
+    (0 ok, 1 non-finite input, 2 not converged within the sweep limit:
+    ``max_sweeps``, 1..30, default 30).  With ``check`` the call synchronizes
+    and raises ``ValueError`` for the first head with a nonzero status."""
     heads = _tiles(provider, torch.float32, "provider state")
     lead = tuple(provider.shape[:-2])
     device = provider.device
@@ -138,16 +142,20 @@ def exact_svd_boundary(provider: torch.Tensor, check: bool = True, residual=None
              "GDN State Codec SVD residual must be a contiguous fp32 buffer of the "
              "provider's size on its device")
     status = torch.empty(lead, dtype=torch.int32, device=device)
-    _check(native().exact_svd_boundary_launch_v1(
-        _stream(), provider.data_ptr(), residual.data_ptr(), codes.data_ptr(),
-        smoothing.data_ptr(), scales.data_ptr(), keys.data_ptr(), values.data_ptr(),
-        status.data_ptr(), heads), "exact SVD boundary")
+    pointers = (_stream(), provider.data_ptr(), residual.data_ptr(), codes.data_ptr(),
+                smoothing.data_ptr(), scales.data_ptr(), keys.data_ptr(), values.data_ptr(),
+                status.data_ptr(), heads)
+    if max_sweeps is None:
+        _check(native().exact_svd_boundary_launch_v1(*pointers), "exact SVD boundary")
+    else:
+        _check(native().exact_svd_boundary_sweeps_launch_v1(*pointers, max_sweeps),
+               "exact SVD boundary")
     if check:
         flat = status.reshape(-1).cpu()
         bad = torch.nonzero(flat).reshape(-1)
         if bad.numel():
             raise ValueError(f"GDN State Codec boundary head {int(bad[0])} "
-                             f"{FIT_STATUS.get(int(flat[int(bad[0])]), 'failed')}")
+                             f"{SVD_STATUS.get(int(flat[int(bad[0])]), 'failed')}")
     return codes, smoothing, scales, keys, values, residual, status
 
 

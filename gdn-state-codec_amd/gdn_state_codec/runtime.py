@@ -422,7 +422,8 @@ class GdnStateCodecRuntime:
         exact-SVD initializer (runtime.py:335-389): fp16 rank-4 compensators
         U*S and V of each dense head's truncated SVD, and the quant-only codes
         of the residual, by one launch of the library's Jacobi SVD.  Raises
-        for a head with a non-finite value."""
+        for a head with a non-finite value or one whose iteration did not
+        converge."""
         boundary = self._provider_boundary(provider_dense)
         heads = provider_dense.shape[0]
         slot = _Slot(boundary)
@@ -433,10 +434,12 @@ class GdnStateCodecRuntime:
             boundary.scales.data_ptr(), boundary.compensator_keys.data_ptr(),
             boundary.compensator_values.data_ptr(), status.data_ptr(), heads),
             "exact SVD initializer")
-        rejected = torch.nonzero(status.cpu()).reshape(-1)
+        flat = status.cpu()
+        rejected = torch.nonzero(flat).reshape(-1)
         if rejected.numel():
-            raise RuntimeError(f"GDN State Codec exact SVD initializer: head "
-                               f"{int(rejected[0])} holds a non-finite value")
+            head = int(rejected[0])
+            raise RuntimeError(f"GDN State Codec exact SVD initializer: head {head} "
+                               f"{codec.SVD_STATUS.get(int(flat[head]), 'failed')}")
         return slot
 
     def _encode_dense_boundary(self, dense: torch.Tensor,

@@ -126,8 +126,11 @@ int32_t statecentric_gdn_state_codec_quantize_boundary_launch_v1(
  * decreasing singular value; residual fp32 [heads][value][key] = the provider
  * tile minus the fp32 rank-4 product; then encode_launch_v4 of the residual in
  * the [value][key] layout (quantized [value][key], smoothing by key,
- * value_scales by value).  status[h] is 0, or 1 when head h holds a
- * non-finite value (its outputs are then unspecified).  The signs of each
+ * value_scales by value).  status[h] is 0; 1 when head h holds a
+ * non-finite value (its outputs are then unspecified); or 2 when the Jacobi
+ * iteration still rotated a pair in its last allowed sweep (30 here): the
+ * outputs are then written from that sweep's rows, an unconverged fit the
+ * caller should not take as the SVD.  The signs of each
  * (U, V) column pair are the iteration's own (an SVD fixes only their
  * product); the iteration runs in double, so the fp32 rank-4 product agrees
  * with a float64 SVD to the fp32 rounding of the outputs (about 1e-7 of the
@@ -137,6 +140,15 @@ int32_t statecentric_gdn_state_codec_exact_svd_boundary_launch_v1(
     void* stream, const float* provider, float* residual, int8_t* quantized,
     float* smoothing, float* value_scales, uint16_t* compensator_keys,
     uint16_t* compensator_values, int32_t* status, uint64_t heads);
+
+/* exact_svd_boundary_launch_v1 with a caller-chosen limit of
+ * 1 <= max_sweeps <= 30 Jacobi sweeps (status 1 for a limit outside it): a
+ * head that has not converged within the limit gets status 2.  For callers
+ * that trade the fit's accuracy for time.  No counterpart in the reference. */
+int32_t statecentric_gdn_state_codec_exact_svd_boundary_sweeps_launch_v1(
+    void* stream, const float* provider, float* residual, int8_t* quantized,
+    float* smoothing, float* value_scales, uint16_t* compensator_keys,
+    uint16_t* compensator_values, int32_t* status, uint64_t heads, uint32_t max_sweeps);
 
 /* Decode of `heads` tiles.  compensator_keys/values are both NULL (quant-only,
  * rank 0) or both fp32 [heads][128][4] (rank 4, the dequantize_launch_v1 form). */

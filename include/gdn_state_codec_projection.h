@@ -14,7 +14,8 @@
  * agree with the fp64 evaluation of the same sum to within
  * 2^-15 * (sum_k |code * s * x|) * scale / 127 (decode) and 2^-14 times the
  * same magnitude (chunked, whose weights s * x enter the bf16 matrix cores as
- * two rounded bf16 parts).
+ * two rounded bf16 parts; the bound holds for every finite weight of
+ * magnitude at least 2^-110, the top of fp32's range included).
  *
  * Same conventions as gdn_state_codec_kernel.h: asynchronous on `stream`, no
  * allocation, status 0 / 1 (bad argument) / 5 (launch failed).

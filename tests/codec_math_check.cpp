@@ -92,6 +92,24 @@ void check_div127() {
   if (to_bits(gdn::div_by_reciprocal(0.0f, b, y)) != to_bits(0.0f / b)) ++failures;
 }
 
+// div_by_127 (the two-part reciprocal) against IEEE a / 127 over the same
+// exponent range as check_div127, plus both zeros.
+void check_div127_split() {
+  const uint64_t lo = static_cast<uint64_t>(27) << 23;
+  const uint64_t hi = static_cast<uint64_t>(248) << 23;
+  parallel(lo, hi, [&](uint64_t u, uint64_t& n, uint64_t& bad) {
+    for (uint32_t sign = 0; sign < 2; ++sign) {
+      const float a = from_bits(static_cast<uint32_t>(u) | (sign << 31));
+      ++n;
+      if (to_bits(gdn::div_by_127(a)) != to_bits(a / 127.0f)) ++bad;
+    }
+  });
+  for (const float a : {0.0f, -0.0f}) {
+    ++checked;
+    if (to_bits(gdn::div_by_127(a)) != to_bits(a / 127.0f)) ++failures;
+  }
+}
+
 void check_div_random(int divisors) {
   srand(12345);
   for (int d = 0; d < divisors; ++d) {
@@ -283,6 +301,8 @@ int main(int argc, char** argv) {
   if (argc < 2) return 2;
   if (strcmp(argv[1], "div127") == 0) {
     check_div127();
+  } else if (strcmp(argv[1], "div127split") == 0) {
+    check_div127_split();
   } else if (strcmp(argv[1], "divrandom") == 0) {
     check_div_random(argc > 2 ? atoi(argv[2]) : 64);
   } else if (strcmp(argv[1], "refit") == 0) {

@@ -125,6 +125,9 @@ def test_windowed_entry_points_admit_like_the_reference(lib):
         assert lib.int8_matmul_launch_v4(None, p, p, p, states, transpose) == 1
     assert lib.int8_matmul_launch_v4(None, None, p, p, 8, 0) == 1
     assert lib.int8_matmul_launch_v4(None, p, p, ctypes.c_void_p(20), 8, 0) == 1
+    # The exact-SVD sweep limit: 1..30.
+    for sweeps in (0, 31):
+        assert lib.exact_svd_boundary_sweeps_launch_v1(None, *[p] * 8, 1, sweeps) == 1
 
 
 def test_decode_runtime_lifecycle(lib):

@@ -45,6 +45,13 @@ def test_division_by_127_is_ieee_on_its_whole_domain(checker):
     assert checked > 3_000_000_000 and failures == 0 and rc == 0
 
 
+def test_two_part_division_by_127_is_ieee_on_its_whole_domain(checker):
+    """div_by_127 (q = RN(a * R + RN(a * L)), the dequantize's division) for
+    every float with 2^-100 <= |a| < 2^121 and both zeros."""
+    rc, checked, failures = _run(checker, "div127split")
+    assert checked > 3_000_000_000 and failures == 0 and rc == 0
+
+
 def test_division_by_random_divisors_is_ieee(checker):
     rc, checked, failures = _run(checker, "divrandom", "48")
     assert checked == 48 * 2 * (1 << 23) and failures == 0 and rc == 0

@@ -4,12 +4,15 @@ src/gdn_state_codec/runtime.py:335-389, which calls torch.linalg.svd) through
 the C-ABI, against the float64 LAPACK SVD of oracle/svd.py.
 
 The reference's result is its library's fp32 SVD, so no bit pattern is fixed;
-the tests hold the fp32 rank-4 product to 2e-6 of the largest singular value
-(the kernel iterates in double, so only the fp32 rounding of its outputs
-remains; torch's fp32 SVD lands at 3e-7..3e-6 on Gaussian heads), the
-singular values likewise, the fp16 compensators to their own rounding of
+the tests hold the fp32 rank-4 product to 4e-7 of the largest singular value,
+the singular values likewise, the fp16 compensators to their own rounding of
 that product, and the codes bit-exact to the oracle's quant stage applied to
-the residual the kernel wrote."""
+the residual the kernel wrote.  The kernel iterates in double, so what remains
+is the fp32 rounding of its outputs: keys and values rounded to fp32 and a
+four-term fp32 product, a few units of 2^-24 of the largest singular value
+(the bench measures 7.3e-8 on C1 heads).  4e-7 leaves that a margin of about
+five, so an accumulation that loses ten times the precision fails; torch's
+fp32 SVD, the reference's own call, lands at 3e-7..3e-6 on Gaussian heads."""
 
 import numpy as np
 import pytest
@@ -21,7 +24,7 @@ from gdn_state_codec import codec
 from oracle import svd as S
 
 pytestmark = pytest.mark.gpu
-FIT_TOLERANCE = 2e-6  # of the largest singular value
+FIT_TOLERANCE = 4e-7  # of the largest singular value
 
 
 def host(t):
@@ -145,3 +148,22 @@ def test_many_heads(device):
     _, got = run(dense)
     sample = list(range(0, len(dense), 61))
     check_heads(dense[sample], [g[sample] for g in got])
+
+
+def test_sweep_limit_flags_unconverged_heads(device):
+    """exact_svd_boundary_sweeps_launch_v1: after one sweep no C1 head has
+    converged (status 2, and exact_svd_boundary raises), while an all-zero
+    head, which never rotates, has (status 0); at the full limit of 30 sweeps
+    every output equals the default entry point's bit for bit."""
+    print("exact SVD sweep limit", flush=True)
+    dense = np.concatenate([datagen.c1_heads(3, 79), np.zeros((1, 128, 128), np.float32)])
+    provider = torch.from_numpy(np.ascontiguousarray(dense.transpose(0, 2, 1))).cuda()
+    *_, status = codec.exact_svd_boundary(provider, check=False, max_sweeps=1)
+    assert host(status).tolist() == [2, 2, 2, 0]
+    with pytest.raises(ValueError, match="did not converge"):
+        codec.exact_svd_boundary(provider, max_sweeps=1)
+    full = [host(t) for t in codec.exact_svd_boundary(provider, max_sweeps=30)]
+    default = [host(t) for t in codec.exact_svd_boundary(provider)]
+    for a, b in zip(full, default):
+        assert a.tobytes() == b.tobytes()
+    assert (full[-1] == 0).all()
