@@ -463,7 +463,8 @@ def bench_window_step(warmup: int):
     """The windowed decode step at B=256 (8192 states): 5 slot copies, each
     stepped through a whole window (positions 0..15) between one event pair,
     launches interleaved across copies so consecutive launches touch different
-    states."""
+    states.  A warm phase of about WARM_MS of whole windows comes first (the
+    projections' warm phase), then the mean over about TIMED_MS of windows."""
     import torch
 
     from gdn_state_codec import codec
@@ -502,30 +503,38 @@ def bench_window_step(warmup: int):
                                                  validate=False),
     }
     results = {}
-    for name, run in kinds.items():
-        for _ in range(max(warmup, 1)):
-            for slot in slots:
-                slot.positions.zero_()
-            for t in range(16):
-                for r in range(ROTATIONS):
-                    run(r)
+
+    def window(run):
+        """One whole window (positions 0..15) of every copy between one event
+        pair; the positions are reset before it, outside the events."""
         for slot in slots:
             slot.positions.zero_()
-        torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for t in range(16):
             for r in range(ROTATIONS):
                 run(r)
         b.record()
+        return a, b
+
+    for name, run in kinds.items():
+        # Warm phase of whole windows, as the projections' (WARM_MS of launches),
+        # then the mean of the timed windows (about TIMED_MS of them).
+        for _ in range(max(warmup, 1)):
+            window(run)
+        estimate_ms = _events_ms([window(run)])[0]
+        for _ in range(min(200, int(WARM_MS / max(estimate_ms, 1e-3)) + 1)):
+            window(run)
+        windows = max(3, min(50, int(TIMED_MS / max(estimate_ms, 1e-3)) + 1))
+        pairs = [window(run) for _ in range(windows)]
         launches = 16 * ROTATIONS
-        us = _events_ms([(a, b)])[0] / launches * 1e3
+        us = sum(_events_ms(pairs)) / (windows * launches) * 1e3
         assert all(bool((slot.positions[:, 0] == 16).all()) for slot in slots)
         compensated = name != "quant_only"
         nbytes = sum(window_step_bytes(p, compensated) for p in range(16)) * states / 16
         results[name] = {"us_per_step": us, "GBps": nbytes / (us * 1e-6) / 1e9,
                          "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
-                         "bytes_per_step": nbytes}
+                         "bytes_per_step": nbytes, "timed_windows": windows}
         _log(f"windowed step {name}: {us:.2f} us/step, {results[name]['GBps']:.0f} GB/s")
     runtime.close()
     results["workload"] = ("windowed bf16 decode step, B=256 x 32 value heads (GQA from 16), "
@@ -592,23 +601,29 @@ def bench_refit(steps: int, warmup: int):
             nxt.scales.data_ptr(), nxt.compensator_keys.data_ptr(),
             nxt.compensator_values.data_ptr(), workspace.data_ptr(), states, power)
 
+    def timed(i, power):
+        r = i % ROTATIONS
+        slot, _, saved = copies[r]
+        slot.positions[:, 0] = 16  # a full window (the power refit clears it)
+        if power:
+            for dst, src in zip((slot.record_decay, slot.record_keys,
+                                 slot.record_corrections), saved):
+                dst.copy_(src)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        assert refit(r, power) == 0
+        b.record()
+        return a, b
+
     results = {}
     for name, power in (("quant_only", 0), ("power", REFIT_POWER_ITERATIONS)):
-        pairs = []
-        for i in range(max(warmup, 1) * ROTATIONS + steps):
-            r = i % ROTATIONS
-            slot, _, saved = copies[r]
-            slot.positions[:, 0] = 16  # a full window (the power refit clears it)
-            if power:
-                for dst, src in zip((slot.record_decay, slot.record_keys,
-                                     slot.record_corrections), saved):
-                    dst.copy_(src)
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            assert refit(r, power) == 0
-            b.record()
-            if i >= max(warmup, 1) * ROTATIONS:
-                pairs.append((a, b))
+        # Warm phase: about WARM_MS of refits (at least `warmup` per copy), as
+        # the projections and the window step get; then `steps` timed refits.
+        first = [timed(i, power) for i in range(max(warmup, 1) * ROTATIONS)]
+        estimate_ms = max(sorted(_events_ms(first))[len(first) // 2], 1e-3)
+        for i in range(min(1000, int(WARM_MS / estimate_ms) + 1)):
+            timed(i, power)
+        pairs = [timed(i, power) for i in range(steps)]
         us = sum(_events_ms(pairs)) / len(pairs) * 1e3
         assert all(bool((c[0].positions[:, 0] == 0).all()) for c in copies)
         nbytes = refit_bytes(power > 0) * states
@@ -752,7 +767,9 @@ def _compression_gate(states: int, copies: int) -> dict:
       finish_encoded_projection) forward and transposed, then prepare -> product ->
       commit_encoded_rank), then encoded_requantize.  The product is
       int8_cube_matmul_launch_v1 at the probe's 32 states and the batched
-      int8_matmul_launch_v4 at B = 256.
+      int8_matmul_launch_v4 at B = 256;
+    * encoded_chain_fused: the same cycle with the rank chain as one launch of
+      encoded_rank_chain_launch_v4 per slot (bit-identical bases).
 
     Positions, fitted bases and nothing else are reset outside the timed
     region, as the probe's restore_cycle / reset_bases do."""
@@ -857,6 +874,20 @@ def _compression_gate(states: int, copies: int) -> dict:
             stream, slots[r].residual.data_ptr(), *operands(r), left.data_ptr(),
             right.data_ptr(), *(t.data_ptr() for t in req), states))
 
+    compact_seeds = seeds[..., 0].permute(1, 0, 2).contiguous()  # [S][4][128]
+    fused_corrected = torch.empty((states, 4, 128), dtype=torch.float32, device=dev)
+
+    def fused_chain(r):
+        left, right = bases[r]
+        s = slots[r]
+        ok(lib.encoded_rank_chain_launch_v4(
+            stream, s.residual.data_ptr(), *operands(r), compact_seeds.data_ptr(),
+            left.data_ptr(), right.data_ptr(), fused_corrected.data_ptr(), states,
+            GATE_CHAIN_ITERATIONS))
+        ok(lib.encoded_requantize_launch_v1(
+            stream, s.residual.data_ptr(), *operands(r), left.data_ptr(),
+            right.data_ptr(), *(t.data_ptr() for t in req), states))
+
     def refit(r, power):
         n = nxt[r]
         ok(lib.window_boundary_launch_v1(
@@ -880,6 +911,8 @@ def _compression_gate(states: int, copies: int) -> dict:
                 refit(r, 0)
             elif kind == "power":
                 refit(r, REFIT_POWER_ITERATIONS)
+            elif kind == "encoded_chain_fused":
+                fused_chain(r)
             else:
                 rank_chain(r)
 
@@ -892,7 +925,7 @@ def _compression_gate(states: int, copies: int) -> dict:
     def restore(kind):
         for r in range(copies):
             slots[r].positions.zero_()
-            if kind == "encoded_chain":
+            if kind.startswith("encoded_chain"):
                 for b in bases[r]:
                     b.zero_()
 
@@ -908,7 +941,7 @@ def _compression_gate(states: int, copies: int) -> dict:
         wall = time.perf_counter() - t0
         return a.elapsed_time(b) * 1e3 / copies, wall * 1e6 / copies
 
-    kinds = ("quant_only", "power", "encoded_chain")
+    kinds = ("quant_only", "power", "encoded_chain", "encoded_chain_fused")
     # Warm phase: whole cycles of every kind until about WARM_MS has run.
     t0 = time.perf_counter()
     while True:

@@ -66,6 +66,7 @@ SIGNATURES: dict[str, list] = {
         [_P] * 14 + [_U32, _U32, _U32],
     "statecentric_gdn_state_codec_commit_encoded_rank_launch_v1": [_P] * 14 + [_U32, _U32],
     "statecentric_gdn_state_codec_encoded_requantize_launch_v1": [_P] * 17 + [_U32],
+    "statecentric_gdn_state_codec_encoded_rank_chain_launch_v4": [_P] * 13 + [_U32, _U32],
     # window-boundary refit
     "statecentric_gdn_state_codec_window_boundary_launch_v1": [_P] * 16 + [_U32, _U32],
     "statecentric_gdn_state_codec_window_boundary_noalloc_launch_v1": [_P] * 15 + [_U32, _U32],

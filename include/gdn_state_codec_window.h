@@ -200,6 +200,28 @@ int32_t statecentric_gdn_state_codec_commit_encoded_rank_launch_v1(
     const uint16_t* record_left, const uint16_t* record_right, uint16_t* new_left,
     uint16_t* new_right, float* corrected, uint32_t states, uint32_t rank);
 
+/* The whole rank chain above in one launch, for callers that would
+ * otherwise issue it stage by stage: for each rank r = 0..3 the vector
+ * seeds[s][r] (fp16 [S][4][128]) is projected and finished forward and
+ * transposed `iterations` times with r fitted ranks, then projected once more
+ * and committed as rank r.  Every stage is the corresponding entry point's
+ * arithmetic (prepare_int8_vector, the int8 product, finish / commit), so
+ * new_left / new_right (fp16 [S][4][128], the layout commit writes) are
+ * bit-identical to the launch-per-stage chain with reset (zero) fitted bases,
+ * and corrected[s][r] (fp32 [S][4][128]) holds column 0 of rank r's commit.
+ * The other operands are those of finish_encoded_projection_launch_v1.  One
+ * 256-thread workgroup per state keeps the vector in LDS and the int8 boundary
+ * in registers, so the [S][128][16] vector arrays are not used.
+ * 1 <= states <= 16384, 1 <= iterations <= 64.  Batched counterpart of the
+ * stage-by-stage chain host/gdn_state_codec_encoded_projection_probe.cpp:
+ * 611-636 drives through windowed_gdn_kernel.h:108-169. */
+int32_t statecentric_gdn_state_codec_encoded_rank_chain_launch_v4(
+    void* stream, const int8_t* residual, const float* smoothing, const float* scales,
+    const uint16_t* old_left, const uint16_t* old_right, const float* record_decay,
+    const uint16_t* record_left, const uint16_t* record_right, const uint16_t* seeds,
+    uint16_t* new_left, uint16_t* new_right, float* corrected, uint32_t states,
+    uint32_t iterations);
+
 /* residual int8 [S][128][128] as [smoothing axis][scale axis]; the window
  * operator minus new_left^T new_right, re-encoded exactly as the rank-4
  * window-boundary refit re-encodes (fresh smoothing, absmax scales,
