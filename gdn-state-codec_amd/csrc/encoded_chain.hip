@@ -65,17 +65,22 @@ struct ChainArgs {
 // axis.  A finish with transpose T takes its input on side T and writes on
 // side 1 - T; the forward product (T = 0) maps a right-side vector to the
 // left side.
+// Basis rows are padded to 132 fp16 (66 words): the 24 coefficient lanes,
+// each reading 8 bytes of its own row, then start on banks 2c and hit 48
+// distinct banks; unpadded 256-byte rows put all 24 on one bank.
+constexpr int kBasisStride = kDim + 4;
+
 struct ChainShared {
   // basis[side][row][dim], fp16: rows 0..3 the old compensators of that side
   // (transposed from [dim][rank]), 4..7 the fitted ranks, 8..23 the records.
-  uint16_t basis[2][kCoefficientRows][kDim];
+  uint16_t basis[2][kCoefficientRows][kBasisStride];
   float axis[2][kDim];
   float decay[kWindow];
   uint16_t vector[kDim];  // the current vector, fp16 bits
-  float x[kDim];          // fp16(vector) widened, for the coefficient sums
-  uint32_t q[kDim / 4];   // the quantized vector, four int8 per word
+  __attribute__((aligned(16))) float x[kDim];  // fp16(vector) widened
+  __attribute__((aligned(16))) uint32_t q[kDim / 4];  // the quantized vector
   int32_t p[kDim];        // the projection
-  float values[kDim];     // the rows' values, for the squared norm
+  __attribute__((aligned(16))) float values[kDim];  // the rows' values, for the norm
   float dynamic_scale;
 };
 
@@ -187,7 +192,13 @@ __device__ void chain_finish(ChainShared& sh, int in_side, uint32_t ranks, int l
   sh.values[lane + kChainLanes] = row_value[1];
   wave_lds_sync();
   float squared_norm = 0.0f;
-  for (int row = 0; row < kDim; ++row) squared_norm += sh.values[row] * sh.values[row];
+  for (int row = 0; row < kDim; row += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(sh.values + row);
+    squared_norm += v.x * v.x;
+    squared_norm += v.y * v.y;
+    squared_norm += v.z * v.z;
+    squared_norm += v.w * v.w;
+  }
   const float inverse = squared_norm > 1.0e-20f ? 1.0f / chain_newton_sqrt(squared_norm) : 0.0f;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -215,7 +226,29 @@ __device__ void chain_commit(ChainShared& sh, const ChainArgs& a, uint64_t state
   }
 }
 
-__global__ __launch_bounds__(kChainThreads, 5) void encoded_chain_kernel(ChainArgs a) {
+// sum over i < 16 of the signed byte dot products of codes[i] and q[i].
+__device__ __forceinline__ int dot64(const uint32_t (&codes)[16], const uint32_t* q) {
+  int acc = 0;
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    const uint4 qw = *reinterpret_cast<const uint4*>(q + i);
+    acc = __builtin_amdgcn_sdot4(static_cast<int>(codes[i]), static_cast<int>(qw.x), acc, false);
+    acc = __builtin_amdgcn_sdot4(static_cast<int>(codes[i + 1]), static_cast<int>(qw.y), acc,
+                                 false);
+    acc = __builtin_amdgcn_sdot4(static_cast<int>(codes[i + 2]), static_cast<int>(qw.z), acc,
+                                 false);
+    acc = __builtin_amdgcn_sdot4(static_cast<int>(codes[i + 3]), static_cast<int>(qw.w), acc,
+                                 false);
+  }
+  return acc;
+}
+
+// Eight waves per SIMD (64 VGPRs): two states per SIMD at a time and 2,048 in
+// flight, so 8,192 states run in four full rounds.  The compiler spills about
+// half of the column words to scratch and reloads them in each transposed
+// product; measured at 8,192 states and 8 iterations (ms): 2.20 at five waves
+// per SIMD without spills, 1.99 at six, 1.76 at eight, bit-identical.
+__global__ __launch_bounds__(kChainThreads, 8) void encoded_chain_kernel(ChainArgs a) {
   __shared__ ChainShared sh;
   const int t = threadIdx.x;
   const int wave = t >> 6;
@@ -236,20 +269,36 @@ __global__ __launch_bounds__(kChainThreads, 5) void encoded_chain_kernel(ChainAr
       const uint4 w = src[i];
       rows[4 * i] = w.x, rows[4 * i + 1] = w.y, rows[4 * i + 2] = w.z, rows[4 * i + 3] = w.w;
     }
+    // The columns through LDS, half the tile at a time, staged in the basis
+    // area before the bases are loaded: rows 64h..64h+63 (8 KiB) are written
+    // by the threads that hold them and read down the columns by the threads
+    // of part h.
+    uint8_t* const stage = reinterpret_cast<uint8_t*>(&sh.basis[0][0][0]);
+    static_assert(sizeof(sh.basis) >= 64 * kDim, "staging area");
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      // Four words' bytes in flight at a time: all 64 at once would hold 64
-      // VGPRs in this prologue.
-      if ((i & 3) == 0) __builtin_amdgcn_sched_barrier(0);
-      uint32_t word = 0;
+    for (int h = 0; h < 2; ++h) {
+      __syncthreads();
+      if ((line >> 6) == h) {
+        uint4* const to = reinterpret_cast<uint4*>(stage + (line - 64 * h) * kDim + 64 * part);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        word |= static_cast<uint32_t>(static_cast<uint8_t>(
-                    tile[(64 * part + 4 * i + j) * kDim + line]))
-                << (8 * j);
+        for (int i = 0; i < 4; ++i) {
+          to[i] = make_uint4(rows[4 * i], rows[4 * i + 1], rows[4 * i + 2], rows[4 * i + 3]);
+        }
       }
-      columns[i] = word;
+      __syncthreads();
+      if (part == h) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            word |= static_cast<uint32_t>(stage[(4 * i + j) * kDim + line]) << (8 * j);
+          }
+          columns[i] = word;
+        }
+      }
     }
+    __syncthreads();  // the staging area becomes the bases
   }
 
   // ---- bases, records, scales, gates, zero fitted ranks --------------------
@@ -284,16 +333,13 @@ __global__ __launch_bounds__(kChainThreads, 5) void encoded_chain_kernel(ChainAr
       __syncthreads();
       if (wave == role) chain_prepare(sh, side, lane);
       __syncthreads();
-      // p[line] over the thread's 64 codes of the line and its partner's 64.
-      const uint32_t* const code = side == 0 ? rows : columns;
+      // p[line] over the thread's 64 codes of the line and its partner's 64
+      // (a uniform branch: one straight loop per orientation, no selects).
       int acc = 0;
-#pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        const uint4 qw = *reinterpret_cast<const uint4*>(&sh.q[16 * part + i]);
-        acc = __builtin_amdgcn_sdot4(static_cast<int>(code[i]), static_cast<int>(qw.x), acc, false);
-        acc = __builtin_amdgcn_sdot4(static_cast<int>(code[i + 1]), static_cast<int>(qw.y), acc, false);
-        acc = __builtin_amdgcn_sdot4(static_cast<int>(code[i + 2]), static_cast<int>(qw.z), acc, false);
-        acc = __builtin_amdgcn_sdot4(static_cast<int>(code[i + 3]), static_cast<int>(qw.w), acc, false);
+      if (side == 0) {
+        acc = dot64(rows, sh.q + 16 * part);
+      } else {
+        acc = dot64(columns, sh.q + 16 * part);
       }
       acc += __builtin_amdgcn_update_dpp(0, acc, 0xB1, 0xF, 0xF, false);  // partner lane t ^ 1
       if (part == 0) sh.p[line] = acc;
