@@ -17,8 +17,9 @@ namespace gdn {
 // to XCD b % 8, so the identity order has the 8 XCDs working on neighbouring
 // tiles at every moment.  This order gives XCD x the contiguous items
 // x * q .. x * q + q - 1 (q = blocks / 8, in order), and the last blocks % 8
-// items to the workgroups past 8 q.  Measured on the config-2 dequantize:
-// 3.26 ms against 3.70 ms in identity order, bit-identical output.
+// items to the workgroups past 8 q.  Measured on the config-2 dequantize
+// (bit-identical output): 3.26 ms against 3.70 ms in identity order on one box,
+// 3.64-3.66 against 3.69-3.71 ms on four others; the gain depends on the box.
 GDN_ORDER_HD uint64_t xcd_contiguous_item(uint64_t block, uint64_t blocks) {
   const uint64_t per_xcd = blocks >> 3;
   if (block >= per_xcd << 3) return block;
