@@ -195,19 +195,31 @@ __global__ __launch_bounds__(kThreads, 8) void decode_projection_kernel(
 //
 // A workgroup owns one (sequence, head) tile; wavefront w owns the 32 values
 // 32w..32w+31 (two 16-column MFMA tiles) and keeps their codes in registers as
-// bf16 for every token block.  Token blocks of 16 rows are staged in LDS as the
-// two bf16 parts of w[t][k] = s[k] * x_t[k] in operand order (8 KiB), so all
-// 2048 workgroups of a 64 x 32-head batch are resident at once.
+// bf16 for every token block.  The tokens are taken kSub blocks of 16 rows at a
+// time: the two bf16 parts of w[t][k] = s[k] * x_t[k] of each 16-row block are
+// staged in LDS in operand order (8 KiB per block), behind one barrier pair per
+// kSub blocks.  With kSub = 2 (17 KiB of LDS, 64 VGPRs) all 2048 workgroups of
+// a 64 x 32-head batch are still resident at once, and each runs half as many
+// barrier-separated rounds of query loads as with kSub = 1: config 4 measured
+// 24.9 -> 23.6 us ([key][value]: 30.8 -> 27.6 us), bit-identical.  kSub = 4
+// (33 KiB) leaves half the grid to a second round (24.6 us).
+//
+// kTail = false requires tokens % (16 * kSub) == 0.  kTail = true handles any
+// token count: rows past the last token are computed from a clamped token
+// (each output row depends only on its own query row) and never stored.
+// Query and output addresses are a per-workgroup base plus a 32-bit lane byte
+// offset, so one sequence's output rows must span fewer than 2^32 bytes
+// (tokens * value_heads * 512; the launcher checks).
 // The [value][key] form fits 64 VGPRs (8 wavefronts per SIMD); the byte gathers
 // of the [key][value] form need more.
-template <uint32_t kLayout>
+template <uint32_t kLayout, int kSub, bool kTail>
 __global__ __launch_bounds__(kThreads, kLayout == kValueKey ? 8 : 4) void chunked_projection_kernel(
     const int8_t* __restrict__ codes, const float* __restrict__ smoothing,
     const float* __restrict__ scales, const uint16_t* __restrict__ queries,
     float* __restrict__ out, uint32_t tokens, uint32_t value_heads,
     uint32_t group, uint32_t query_heads, float query_scale) {
   constexpr int kBlockTokens = 16;
-  __shared__ uint4 a_lds[2][4][64];  // [part][k-step][lane] x 8 bf16
+  __shared__ uint4 a_lds[kSub][2][4][64];  // [block][part][k-step][lane] x 8 bf16
   __shared__ float s_lds[kDim];
   __shared__ __align__(16) float e_lds[kDim];  // scale[v] / 127
 
@@ -258,86 +270,102 @@ __global__ __launch_bounds__(kThreads, kLayout == kValueKey ? 8 : 4) void chunke
     e_lds[t] = scales[pair * kDim + t] / kQuantizedMaximum;
   }
 
-  // Producer role: thread t builds token row m = t / 16 of the block, keys
+  // Producer role: thread t builds token row m = t / 16 of each block, keys
   // 8*kc..+7 (kc = t % 16), which is k-step kc % 4 of lane group kc / 4.
   const int m = t >> 4;
   const int kc = t & 15;
   const int dst_lane = m + 16 * (kc >> 2);
   const int dst_step = kc & 3;
+  // Per-workgroup bases (uniform, scalar registers) plus per-lane 32-bit byte
+  // offsets: the loads and stores take the scalar-base addressing form.
+  const char* const q_seq =
+      reinterpret_cast<const char*>(queries + (n * tokens * query_heads + qh) * kDim);
+  const uint32_t q_row = query_heads * kDim * 2;  // bytes per token
+  char* const o_seq = reinterpret_cast<char*>(out + (n * tokens * value_heads + h) * kDim);
+  const uint32_t o_row = value_heads * kDim * 4;
+  const bool odd = (col & 1) != 0;
+  const int first = 32 * wave + (odd ? 15 + col : col);
+  // Running lane offsets of the round's first block (query row m, output row
+  // 4g, value `first`); the sub-block and row steps are uniform.  Offsets that
+  // change every round keep the compiler from holding one per sub-block and
+  // row in registers.
+  uint32_t q_off = m * q_row + 16 * kc;
+  uint32_t o_off = 4 * g * o_row + 4 * first;
+  const uint32_t q_last = (tokens - 1) * q_row + 16 * kc;  // query row tokens - 1
 
-  for (uint32_t block = 0; block < tokens; block += kBlockTokens) {
-    __syncthreads();  // s_lds ready / previous block's operands consumed
-    const uint32_t token = block + m;
-    uint4 qv = make_uint4(0, 0, 0, 0);
-    if (token < tokens) {
-      qv = *reinterpret_cast<const uint4*>(
-          queries + ((n * tokens + token) * query_heads + qh) * kDim + 8 * kc);
-    }
-    const float4 s0 = *reinterpret_cast<const float4*>(s_lds + 8 * kc);
-    const float4 s1 = *reinterpret_cast<const float4*>(s_lds + 8 * kc + 4);
-    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-    uint32_t hi[4], lo[4];
+  for (uint32_t block = 0; block < tokens; block += kSub * kBlockTokens) {
+    __syncthreads();  // s_lds ready / previous blocks' operands consumed
+    uint4 qv[kSub];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t word = word_of(qv, p);
-      const float w0 = sv[2 * p] * (query_scale * bf16_to_float(word & 0xFFFFu));
-      const float w1 = sv[2 * p + 1] * (query_scale * bf16_to_float(word >> 16));
-      split2_pair(w0, w1, hi[p], lo[p]);
+    for (int sub = 0; sub < kSub; ++sub) {
+      uint32_t offset = q_off + kBlockTokens * sub * q_row;
+      if constexpr (kTail) offset = min(offset, q_last);  // token clamped to tokens - 1
+      qv[sub] = *reinterpret_cast<const uint4*>(q_seq + offset);
     }
-    a_lds[0][dst_step][dst_lane] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-    a_lds[1][dst_step][dst_lane] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+#pragma unroll
+    for (int sub = 0; sub < kSub; ++sub) {
+      const float4 s0 = *reinterpret_cast<const float4*>(s_lds + 8 * kc);
+      const float4 s1 = *reinterpret_cast<const float4*>(s_lds + 8 * kc + 4);
+      const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+      uint32_t hi[4], lo[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t word = word_of(qv[sub], p);
+        const float w0 = sv[2 * p] * (query_scale * bf16_to_float(word & 0xFFFFu));
+        const float w1 = sv[2 * p + 1] * (query_scale * bf16_to_float(word >> 16));
+        split2_pair(w0, w1, hi[p], lo[p]);
+      }
+      a_lds[sub][0][dst_step][dst_lane] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+      a_lds[sub][1][dst_step][dst_lane] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    }
     __syncthreads();
 
-    f32x4 acc[2];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int sub = 0; sub < kSub; ++sub) {
+      const uint32_t rows = block + kBlockTokens * sub;  // first token of the block
+      if (kTail && rows >= tokens) break;
+      f32x4 acc[2];
 #pragma unroll
-    for (int step = 0; step < 4; ++step) {
+      for (int c = 0; c < 2; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        const bf16x8 a = __builtin_bit_cast(bf16x8, a_lds[part][step][lane]);
+      for (int step = 0; step < 4; ++step) {
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[c][step], acc[c],
-                                                           0, 0, 0);
+        for (int part = 0; part < 2; ++part) {
+          const bf16x8 a = __builtin_bit_cast(bf16x8, a_lds[sub][part][step][lane]);
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[c][step], acc[c],
+                                                             0, 0, 0);
+          }
+        }
+      }
+      // Accumulator r of column tile c is token row 4g + r of the block, value
+      // 32 wave + 16 c + col.  Adjacent lanes swap one value (DPP quad_perm
+      // [1,0,3,2]) so that the even lane of a pair holds values col, col + 1 of
+      // tile 0 and the odd lane values col - 1, col of tile 1: each store then
+      // writes the wave's 32 values of a row as one whole 128-byte line.
+      const float2 factor = *reinterpret_cast<const float2*>(&e_lds[first]);
+      uint2 pairs[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float send = odd ? acc[0][r] : acc[1][r];
+        const float got = __builtin_bit_cast(
+            float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, send), 0xB1, 0xF,
+                                               0xF, false));
+        const float lo = odd ? got : acc[0][r];
+        const float hi = odd ? acc[1][r] : got;
+        pairs[r] = make_uint2(__float_as_uint(lo * factor.x), __float_as_uint(hi * factor.y));
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (!kTail || rows + 4 * g + r < tokens) {
+          stream_store(reinterpret_cast<uint2*>(o_seq + o_off + (kBlockTokens * sub + r) * o_row),
+                       pairs[r]);
         }
       }
     }
-    // Accumulator r of column tile c is token row 4g + r of the block, value
-    // 32 wave + 16 c + col.  Adjacent lanes swap one value (DPP quad_perm
-    // [1,0,3,2]) so that the even lane of a pair holds values col, col + 1 of
-    // tile 0 and the odd lane values col - 1, col of tile 1: each store then
-    // writes the wave's 32 values of a row as one whole 128-byte line.
-    const bool odd = (col & 1) != 0;
-    const int first = 32 * wave + (odd ? 15 + col : col);
-    const float2 factor = *reinterpret_cast<const float2*>(&e_lds[first]);
-    const uint64_t row_stride = static_cast<uint64_t>(value_heads) * kDim;
-    float* const lane_out = out + ((n * tokens + block) * value_heads + h) * kDim +
-                            4 * g * row_stride + first;
-    uint2 pairs[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float send = odd ? acc[0][r] : acc[1][r];
-      const float got = __builtin_bit_cast(
-          float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, send), 0xB1, 0xF, 0xF,
-                                             false));
-      const float lo = odd ? got : acc[0][r];
-      const float hi = odd ? acc[1][r] : got;
-      pairs[r] = make_uint2(__float_as_uint(lo * factor.x), __float_as_uint(hi * factor.y));
-    }
-    if (block + kBlockTokens <= tokens) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        stream_store(reinterpret_cast<uint2*>(lane_out + r * row_stride), pairs[r]);
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (block + 4 * g + r < tokens) {
-          stream_store(reinterpret_cast<uint2*>(lane_out + r * row_stride), pairs[r]);
-        }
-      }
-    }
+    q_off += kSub * kBlockTokens * q_row;
+    o_off += kSub * kBlockTokens * o_row;
   }
 }
 
@@ -399,16 +427,29 @@ statecentric_gdn_state_codec_encoded_projection_chunked_launch_v4(
   }
   const uint64_t pairs = static_cast<uint64_t>(seqs) * value_heads;
   if (pairs > gdn::kMaxGrid) return gdn::kStatusInvalidArgument;
+  // One sequence's query and output rows are addressed with 32-bit byte
+  // offsets (value_heads >= query_heads, fp32 outputs >= bf16 queries).
+  if (static_cast<uint64_t>(tokens) * value_heads * gdn::kDim * sizeof(float) > 0xFFFFFFFFull) {
+    return gdn::kStatusInvalidArgument;
+  }
   const uint32_t group = value_heads / query_heads;
   const dim3 grid(static_cast<uint32_t>(pairs));
   const dim3 block(gdn::kThreads);
+  // 32-token rounds when every round is full, else 16-token rounds with the
+  // tail handled.
+  const bool whole = tokens % 32 == 0;
   if (layout == gdn::kValueKey) {
-    return gdn::launch(gdn::chunked_projection_kernel<gdn::kValueKey>, grid,
-                       block, stream, residual, smoothing, scales, queries,
-                       outputs, tokens, value_heads, group, query_heads,
-                       query_scale);
+    return whole ? gdn::launch(gdn::chunked_projection_kernel<gdn::kValueKey, 2, false>, grid,
+                               block, stream, residual, smoothing, scales, queries, outputs,
+                               tokens, value_heads, group, query_heads, query_scale)
+                 : gdn::launch(gdn::chunked_projection_kernel<gdn::kValueKey, 1, true>, grid,
+                               block, stream, residual, smoothing, scales, queries, outputs,
+                               tokens, value_heads, group, query_heads, query_scale);
   }
-  return gdn::launch(gdn::chunked_projection_kernel<gdn::kKeyValue>, grid, block,
-                     stream, residual, smoothing, scales, queries, outputs,
-                     tokens, value_heads, group, query_heads, query_scale);
+  return whole ? gdn::launch(gdn::chunked_projection_kernel<gdn::kKeyValue, 2, false>, grid,
+                             block, stream, residual, smoothing, scales, queries, outputs,
+                             tokens, value_heads, group, query_heads, query_scale)
+               : gdn::launch(gdn::chunked_projection_kernel<gdn::kKeyValue, 1, true>, grid,
+                             block, stream, residual, smoothing, scales, queries, outputs,
+                             tokens, value_heads, group, query_heads, query_scale);
 }

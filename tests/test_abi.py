@@ -87,6 +87,9 @@ def test_null_and_out_of_range_arguments_return_status_1(lib):
     assert lib.encoded_projection_decode_launch_v4(None, p, p, p, p, p, 0, 32, 16, 1.0, 1) == 1
     assert lib.encoded_projection_chunked_launch_v4(None, p, p, p, p, p, 1, 0, 32, 16, 1.0, 1) == 1
     assert lib.encoded_projection_chunked_launch_v4(None, p, p, p, p, p, 1, 4, 32, 16, 1.0, 7) == 1
+    # One sequence's output rows must span fewer than 2^32 bytes (32-bit lane offsets).
+    assert lib.encoded_projection_chunked_launch_v4(None, p, p, p, p, p, 1, 1 << 18, 32, 16,
+                                                    1.0, 1) == 1
 
 
 def test_windowed_entry_points_admit_like_the_reference(lib):

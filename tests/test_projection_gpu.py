@@ -121,6 +121,22 @@ def test_chunked_projection_full_config4(device):
     assert _within(got, out64, bound, CHUNKED_TOL).all()
 
 
+@pytest.mark.parametrize("layout", [VK, KV])
+def test_chunked_rounds_of_32_and_16_tokens_agree(device, layout):
+    """Token counts that are multiples of 32 take 32-token rounds, others
+    16-token rounds with a clamped tail: the first 64 outputs of a 65-token
+    call (16-token rounds) equal a 64-token call (32-token rounds) bit for
+    bit, since each output row depends only on its own query row."""
+    codes, s, sc = _encoded((3, 8), 90, layout)
+    q = _queries((3, 65, 4, 128), 91)
+    g = [to_gpu(a, device) for a in (codes, s, sc)]
+    q65 = to_gpu(q, device).view(torch.bfloat16)
+    q64 = to_gpu(np.ascontiguousarray(q[:, :64]), device).view(torch.bfloat16)
+    out65 = codec.project_chunked(*g, q65, 0.75, layout)
+    out64 = codec.project_chunked(*g, q64, 0.75, layout)
+    assert torch.equal(out65[:, :64], out64)
+
+
 def test_chunked_error_is_far_inside_its_bound(device):
     """The two-part split's worst case is 2^-16 of sum |terms| per output; on
     config-4 shaped data the largest error over 2M outputs stays below it, 4x
