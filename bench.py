@@ -47,7 +47,12 @@ C4_FLOPS = 2 * 64 * 64 * 32 * 128 * 128
 ROTATIONS = 5
 # Back-to-back timing of the short kernels: warm-up and minimum timed launches
 # (the profile pass, which only needs a few launches per kernel, lowers them).
-WARM_MS, WARM_LAUNCHES = 100.0, 4000
+# The warm phase runs about 1.2 s of the leg's own launches: for about a second
+# after a heavy leg (the config-2 codec, the HBM probes) the config-4 projection
+# ran at 24.9-25.3 us per launch and then settled at 23.2-23.9 us while still
+# launching back to back (measured in 100 ms windows); with a 100 ms warm phase
+# the bench reported the unsettled figure.
+WARM_MS, WARM_LAUNCHES = 1200.0, 60000
 TIMED_MS, TIMED_LAUNCHES = 30.0, 1000
 PROBE_TILES = 65536
 PROBE_TILE_BYTES = PROBE_TILES * (128 * 128 * 4 + 128 * 128)
@@ -265,12 +270,15 @@ def _time_back_to_back(fn, calls, steps: int) -> float:
     through the argument tuples `calls` (one per rotated state copy), between
     one event pair: the per-step time of a loop issuing one launch after
     another.  The entry point is called with prepared arguments so that the
-    host keeps ahead of the GPU.  A warm phase of the same launches first
-    brings the GPU to its sustained clocks, which a short timed region right
-    after an idle host-side phase would not see (the clocks of 25 us kernels
-    were measured to keep rising for some 30 ms of continuous launches): about
-    WARM_MS of launches, at most WARM_LAUNCHES.  The timed region is at least
-    `steps` launches per copy and about TIMED_MS, at most TIMED_LAUNCHES."""
+    host keeps ahead of the GPU (about 4 us of host time per launch, against
+    23-25 us per config-3/4 launch).  A warm phase of the same launches first
+    brings the GPU to the kernel's own steady state, which a short timed region
+    right after an idle host-side phase or another heavy leg would not see: the
+    clocks of 25 us kernels keep rising for some 30 ms of continuous launches,
+    and the state a heavy leg leaves behind takes about a second to settle.  It
+    runs about WARM_MS of launches, at most WARM_LAUNCHES.  The timed region is
+    at least `steps` launches per copy and about TIMED_MS, at most
+    TIMED_LAUNCHES."""
     import torch
 
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -523,7 +531,7 @@ def bench_window_step(warmup: int):
         for _ in range(max(warmup, 1)):
             window(run)
         estimate_ms = _events_ms([window(run)])[0]
-        for _ in range(min(200, int(WARM_MS / max(estimate_ms, 1e-3)) + 1)):
+        for _ in range(min(3000, WARM_LAUNCHES, int(WARM_MS / max(estimate_ms, 1e-3)) + 1)):
             window(run)
         windows = max(3, min(50, int(TIMED_MS / max(estimate_ms, 1e-3)) + 1))
         pairs = [window(run) for _ in range(windows)]
@@ -621,7 +629,7 @@ def bench_refit(steps: int, warmup: int):
         # the projections and the window step get; then `steps` timed refits.
         first = [timed(i, power) for i in range(max(warmup, 1) * ROTATIONS)]
         estimate_ms = max(sorted(_events_ms(first))[len(first) // 2], 1e-3)
-        for i in range(min(1000, int(WARM_MS / estimate_ms) + 1)):
+        for i in range(min(10000, WARM_LAUNCHES, int(WARM_MS / estimate_ms) + 1)):
             timed(i, power)
         pairs = [timed(i, power) for i in range(steps)]
         us = sum(_events_ms(pairs)) / len(pairs) * 1e3
@@ -1795,6 +1803,13 @@ def _box_info(with_smi: bool = True) -> dict:
         for name in _SYSFS_FIELDS:
             try:
                 fields[name] = (card / name).read_text().strip()
+            except OSError:
+                pass
+        # Board power limits (hwmon, microwatts): a lower cap on some boxes
+        # would show as a lower shader clock under the write-heavy dequantize.
+        for path in sorted(card.glob("hwmon/hwmon*/power*_cap*")):
+            try:
+                fields[path.name] = path.read_text().strip()
             except OSError:
                 pass
         if fields:

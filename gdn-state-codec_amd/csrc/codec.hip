@@ -9,12 +9,14 @@
 //   code     = scale == 0 ? 0 : lround(m / scale * 127)      (clamped to +-127)
 //   dense    = ((s[k] * code) / 127) * scale[v] (+ sum_r ck[k][r] * cv[v][r])
 //
-// One workgroup of 256 threads (4 wavefronts) owns one 128x128 tile.  Thread t
-// holds rows 8j + t/32 (j = 0..15) and the four consecutive columns
+// Encode: one workgroup of 256 threads (4 wavefronts) owns one 128x128 tile.
+// Thread t holds rows 8j + t/32 (j = 0..15) and the four consecutive columns
 // 4*(t%32)..+3 of each, so every load instruction of a wavefront reads 1 KiB of
-// contiguous HBM and every code store writes 256 contiguous bytes.  "Row" and
-// "column" are the tile's memory-major and minor axes; which of them is the key
-// axis depends on the layout.
+// contiguous HBM and every code store writes 256 contiguous bytes.  Decode:
+// one workgroup of 16 (fp32 output) or 8 (bf16 output) wavefronts owns a tile,
+// with the same column quads and fewer rows per thread (DecodeShape).  "Row"
+// and "column" are the tile's memory-major and minor axes; which of them is the
+// key axis depends on the layout.
 //
 // The smoothing sum is order-dependent only when some partial sum needs more
 // than 53 bits.  All terms are non-negative multiples of 2^(e_min-23) (e_min:
@@ -594,19 +596,40 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   }
 }
 
+// Decode thread layouts.  kWaves wavefronts per tile; a lane handles rows
+// row(j) of the tile, j = 0 .. 64 / kWaves - 1, and the four columns
+// 4*(lane%32)..+3, so every store instruction writes two whole rows of
+// contiguous HBM.  With g = thread / 32:
+//   interleaved: row(j) = 2 kWaves j + g (the wavefronts advance together);
+//   bands:       row(j) = (128 / kWaves)(g / 2) + 2j + g % 2 (each wavefront
+//                writes its own contiguous band of 128 / kWaves rows).
+template <int kWaves, bool kBands>
+struct DecodeShape {
+  static constexpr int kThreadCount = 64 * kWaves;
+  static constexpr int kRows = 64 / kWaves;  // rows per thread
+  __device__ static int first_row(int t) {
+    const int g = t >> 5;
+    return kBands ? (kDim / kWaves) * (g >> 1) + (g & 1) : g;
+  }
+  static constexpr int kRowStep = kBands ? 2 : 2 * kWaves;
+};
+
 // dense = ((s[k] * code) / 127) * scale[v] (+ sum_r ck[k][r] * cv[v][r]) for
-// the thread's 16 rows x 4 columns.  kFast selects the reciprocal division.
-template <uint32_t kLayout, bool kFast, bool kCompensated, typename Out>
+// the thread's rows x 4 columns.  kFast selects the two-operation division.
+template <uint32_t kLayout, bool kFast, bool kCompensated, typename Shape, typename Out>
 __device__ __forceinline__ void decode_rows(const int8_t* tile,
                                             const float* s_shared,
                                             const float* scale_shared,
                                             const float* ck_shared,
-                                            const float* cv_shared, int group,
+                                            const float* cv_shared, int first,
                                             int c4, Out* out) {
   constexpr int kRank = 4;
-#pragma unroll 4
-  for (int j = 0; j < kRowsPerThread; ++j) {
-    const int row = 8 * j + group;
+  // The IEEE path (s outside the two-part division's domain) is rare; it
+  // stays rolled so that it does not set the kernel's register count.
+  constexpr int kUnroll = kFast ? (kCompensated ? 2 : 4) : 1;
+#pragma unroll kUnroll
+  for (int j = 0; j < Shape::kRows; ++j) {
+    const int row = first + Shape::kRowStep * j;
     const uint32_t packed =
         stream_load(reinterpret_cast<const uint32_t*>(tile + row * kDim + 4 * c4));
     float v[4];
@@ -636,8 +659,8 @@ __device__ __forceinline__ void decode_rows(const int8_t* tile,
   }
 }
 
-template <uint32_t kLayout, typename Out, bool kCompensated>
-__global__ __launch_bounds__(kThreads) void decode_kernel(
+template <uint32_t kLayout, typename Out, bool kCompensated, typename Shape>
+__global__ __launch_bounds__(Shape::kThreadCount) void decode_kernel(
     const int8_t* __restrict__ codes, const float* __restrict__ smoothing,
     const float* __restrict__ scales,
     const float* __restrict__ compensator_keys,
@@ -654,7 +677,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   if (!pool_entry(map, item, &entry)) return;  // uniform over the workgroup
 
   const int t = threadIdx.x;
-  const int group = t >> 5;
   const int c4 = t & 31;
 
   bool ok = true;
@@ -665,11 +687,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     // is in [2^-90, 2^100]: the product is +-0 or between 2^-90 and 2^107 in
     // magnitude, so its low part a * 2^-35 stays a normal float.
     ok = s >= 0x1p-90f && s <= 0x1p100f;
-  } else {
+  } else if (t < 2 * kDim) {
     scale_shared[t - kDim] = scales[item * kDim + (t - kDim)];
   }
   if constexpr (kCompensated) {
-    for (int i = t; i < kDim * kRank; i += kThreads) {
+    for (int i = t; i < kDim * kRank; i += Shape::kThreadCount) {
       ck_shared[i] = compensator_keys[item * kDim * kRank + i];
       cv_shared[i] = compensator_values[item * kDim * kRank + i];
     }
@@ -678,14 +700,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
 
   const int8_t* tile = codes + item * kTile;
   Out* out = dense + entry * kTile;
+  const int first = Shape::first_row(t);
   if (fast_divide) {
-    decode_rows<kLayout, true, kCompensated>(tile, s_shared, scale_shared,
-                                             ck_shared, cv_shared, group, c4,
-                                             out);
+    decode_rows<kLayout, true, kCompensated, Shape>(tile, s_shared, scale_shared, ck_shared,
+                                                    cv_shared, first, c4, out);
   } else {
-    decode_rows<kLayout, false, kCompensated>(tile, s_shared, scale_shared,
-                                              ck_shared, cv_shared, group, c4,
-                                              out);
+    decode_rows<kLayout, false, kCompensated, Shape>(tile, s_shared, scale_shared, ck_shared,
+                                                     cv_shared, first, c4, out);
   }
 }
 
@@ -718,32 +739,59 @@ int32_t launch_encode(void* stream, const void* source, uint32_t dtype,
                       map);
 }
 
+template <bool kCompensated, typename Shape>
+int32_t launch_decode_shaped(void* stream, const int8_t* codes, const float* smoothing,
+                             const float* scales, const float* compensator_keys,
+                             const float* compensator_values, void* dense,
+                             uint32_t dtype, uint64_t items, uint32_t layout,
+                             TileMap map) {
+  const dim3 grid(static_cast<uint32_t>(items));
+  const dim3 block(Shape::kThreadCount);
+  if (dtype == kDtypeF32) {
+    float* dst = static_cast<float*>(dense);
+    return layout == kKeyValue
+               ? launch(decode_kernel<kKeyValue, float, kCompensated, Shape>, grid,
+                        block, stream, codes, smoothing, scales,
+                        compensator_keys, compensator_values, dst, map)
+               : launch(decode_kernel<kValueKey, float, kCompensated, Shape>, grid,
+                        block, stream, codes, smoothing, scales,
+                        compensator_keys, compensator_values, dst, map);
+  }
+  uint16_t* dst = static_cast<uint16_t*>(dense);
+  return layout == kKeyValue
+             ? launch(decode_kernel<kKeyValue, uint16_t, kCompensated, Shape>, grid,
+                      block, stream, codes, smoothing, scales,
+                      compensator_keys, compensator_values, dst, map)
+             : launch(decode_kernel<kValueKey, uint16_t, kCompensated, Shape>, grid,
+                      block, stream, codes, smoothing, scales,
+                      compensator_keys, compensator_values, dst, map);
+}
+
+// Thread layout per output type, from A/B runs on one box (ms, bit-identical;
+// wavefronts per tile, interleaved or in bands):
+//   config-2 dequantize (fp32, [key][value]): 4 interleaved 3.647, 4 bands
+//     3.543, 8 interleaved 3.584, 8 bands 3.515, 16 bands 3.536,
+//     16 interleaved 3.370;
+//   config-5 fp32 decode-scatter ([value][key] into slots): 4 interleaved
+//     6.234, 8 interleaved 5.928, 8 bands 6.512, 16 bands 5.683,
+//     16 interleaved 5.690;
+//   config-5 bf16 decode-scatter: 4 interleaved 3.627, 8 interleaved 3.562,
+//     8 bands 4.523, 16 bands 3.913, 16 interleaved 3.883.
+// fp32 tiles take 16 interleaved wavefronts (1024 threads, 4 rows per thread),
+// bf16 tiles 8 (512 threads, 8 rows per thread).
 template <bool kCompensated>
 int32_t launch_decode(void* stream, const int8_t* codes, const float* smoothing,
                       const float* scales, const float* compensator_keys,
                       const float* compensator_values, void* dense,
                       uint32_t dtype, uint64_t items, uint32_t layout,
                       TileMap map) {
-  const dim3 grid(static_cast<uint32_t>(items));
-  const dim3 block(kThreads);
-  if (dtype == kDtypeF32) {
-    float* dst = static_cast<float*>(dense);
-    return layout == kKeyValue
-               ? launch(decode_kernel<kKeyValue, float, kCompensated>, grid,
-                        block, stream, codes, smoothing, scales,
-                        compensator_keys, compensator_values, dst, map)
-               : launch(decode_kernel<kValueKey, float, kCompensated>, grid,
-                        block, stream, codes, smoothing, scales,
-                        compensator_keys, compensator_values, dst, map);
-  }
-  uint16_t* dst = static_cast<uint16_t*>(dense);
-  return layout == kKeyValue
-             ? launch(decode_kernel<kKeyValue, uint16_t, kCompensated>, grid,
-                      block, stream, codes, smoothing, scales,
-                      compensator_keys, compensator_values, dst, map)
-             : launch(decode_kernel<kValueKey, uint16_t, kCompensated>, grid,
-                      block, stream, codes, smoothing, scales,
-                      compensator_keys, compensator_values, dst, map);
+  return dtype == kDtypeF32
+             ? launch_decode_shaped<kCompensated, DecodeShape<16, false>>(
+                   stream, codes, smoothing, scales, compensator_keys, compensator_values,
+                   dense, dtype, items, layout, map)
+             : launch_decode_shaped<kCompensated, DecodeShape<8, false>>(
+                   stream, codes, smoothing, scales, compensator_keys, compensator_values,
+                   dense, dtype, items, layout, map);
 }
 
 constexpr TileMap kIdentityMap{nullptr, 0, 0, 0, false};
