@@ -129,7 +129,7 @@ def _probe_library():
         getattr(lib, name).restype = ctypes.c_int32
     lib.gdn_hbm_probe_write.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_uint64, ctypes.c_uint32]
     lib.gdn_hbm_probe_write.restype = ctypes.c_int32
-    for name in ("gdn_hbm_probe_expand", "gdn_hbm_probe_contract"):
+    for name in ("gdn_hbm_probe_expand", "gdn_hbm_probe_contract", "gdn_hbm_probe_halve"):
         getattr(lib, name).argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_uint64, ctypes.c_uint32]
         getattr(lib, name).restype = ctypes.c_int32
     lib.gdn_hbm_probe_grid.restype = ctypes.c_uint32
@@ -176,8 +176,9 @@ def bench_hbm_probe(repeats: int = 5):
     the dispatcher's interleaved order and in the XCD-contiguous order the codec
     kernels use (XCD x streams the x-th eighth of the buffer): copy, read,
     write, and the codec-shaped mixed streams expand (1:4 read:write, a 16 KiB
-    byte tile in and a 64 KiB fp32 tile out per workgroup, the dequantize's mix)
-    and contract (4:1, the quantize's mix)."""
+    byte tile in and a 64 KiB fp32 tile out per workgroup, the dequantize's mix),
+    contract (4:1, the quantize's mix) and halve (2:1, a 32 KiB bf16 tile in and
+    a 16 KiB byte tile out, the bf16 pool encode's mix)."""
     import torch
 
     lib = _probe_library()
@@ -201,6 +202,10 @@ def bench_hbm_probe(repeats: int = 5):
                                                         PROBE_TILES, mode), PROBE_TILE_BYTES),
             "contract": (lambda: lib.gdn_hbm_probe_contract(stream, src.data_ptr(), dst.data_ptr(),
                                                             PROBE_TILES, mode), PROBE_TILE_BYTES),
+            # 65,536 tiles: 2 GiB of bf16 -> 1 GiB of bytes (the bf16 pool encode's mix).
+            "halve": (lambda: lib.gdn_hbm_probe_halve(stream, src.data_ptr(), dst.data_ptr(),
+                                                      PROBE_TILES, mode),
+                      PROBE_TILES * (128 * 128 * 2 + 128 * 128)),
         }
         for name, (fn, moved) in launches.items():
             for _ in range(2):
@@ -1482,6 +1487,21 @@ def pool_bytes_per_direction(dtype_bytes: int) -> int:
     return (POOL_BATCH - POOL_PADDING) * POOL_LAYERS * POOL_HEADS * per_head
 
 
+def _warm_for(fn, warmup: int) -> None:
+    """At least `warmup` calls of `fn`, continued until about WARM_MS has
+    run (at most WARM_LAUNCHES calls): the same warm phase the back-to-back
+    legs get, for legs whose launches are timed one by one."""
+    import torch
+
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    fn()
+    b.record()
+    estimate_ms = max(_events_ms([(a, b)])[0], 1e-3)
+    for _ in range(max(warmup - 1, min(WARM_LAUNCHES, int(WARM_MS / estimate_ms)))):
+        fn()
+
+
 def bench_pool(steps: int, warmup: int, dtype_name: str, cpu: bool = True):
     """Config 5: a [30 layers][2048 slots][32 heads][128][128] state pool in
     the provider's [value][key] layout (fp32 128.8 GB or bf16 64.4 GB),
@@ -1490,7 +1510,8 @@ def bench_pool(steps: int, warmup: int, dtype_name: str, cpu: bool = True):
     compact codes) and decode-scatter (codes -> pool) are timed separately,
     each launch between its own HIP events.  Every encode, warm-up included,
     runs before the first decode, so each one reads the pool as generated;
-    the decodes then write the same values back on every launch.  A sample of
+    the decodes then write the same values back on every launch.  Each
+    direction first warms for about WARM_MS of its own launches.  A sample of
     the gathered tiles (the first live tiles in batch order) is checked bit
     for bit in both directions and timed on the host as the CPU baseline."""
     import torch
@@ -1527,8 +1548,7 @@ def bench_pool(steps: int, warmup: int, dtype_name: str, cpu: bool = True):
     s = torch.empty((layers, batch, heads, 128), dtype=torch.float32, device=dev)
     sc = torch.empty_like(s)
 
-    for _ in range(warmup):
-        codec.pool_encode(pool, perm, layout, codes, s, sc)
+    _warm_for(lambda: codec.pool_encode(pool, perm, layout, codes, s, sc), warmup)
     enc = []
     for _ in range(steps):
         e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
@@ -1538,8 +1558,7 @@ def bench_pool(steps: int, warmup: int, dtype_name: str, cpu: bool = True):
         enc.append((e0, e1))
     enc_ms = sum(_events_ms(enc)) / steps
     sample = _pool_sample(pool, perm, codes, s, sc) if cpu else None
-    for _ in range(warmup):
-        codec.pool_decode(codes, s, sc, perm, pool, layout)
+    _warm_for(lambda: codec.pool_decode(codes, s, sc, perm, pool, layout), warmup)
     dec = []
     for _ in range(steps):
         e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
@@ -1943,6 +1962,22 @@ def codec_roofline(enc_ms: float, dec_ms: float) -> dict:
     return {**kernels[dominant], "dominant": True, "kernels": kernels}
 
 
+def _pool_probe_fractions(pool: dict, probe) -> None:
+    """Each config-5 direction against the same run's tile-stream probe of its
+    read:write mix (the fastest of its four forms): the fp32 encode against the
+    4:1 contract probe, the fp32 decode against the 1:4 expand probe, the bf16
+    encode against the 2:1 halve probe."""
+    if not probe:
+        return
+    def ceiling(name):
+        return max(probe[f"{name}{suffix}_GBps"] for suffix in ("", "_nt", "_xcd", "_nt_xcd"))
+    for dtype, key, name in (("f32", "encode", "contract"), ("f32", "decode", "expand"),
+                             ("bf16", "encode", "halve")):
+        leg = pool[dtype]
+        leg[f"{key}_probe"] = {"kind": name, "GBps": ceiling(name),
+                               "frac": leg[f"{key}_GBps"] / ceiling(name)}
+
+
 def _expand_probe_fraction(probe, dec_gbps: float) -> dict:
     """The dequantize against the 1:4 read:write probe of the same run (the
     fastest of its plain and nontemporal forms in either order): the ceiling of
@@ -2083,6 +2118,7 @@ def main() -> int:
                         "unique slot ids with 26 padding (-1), Student-t(3) x 0.05, 2% zero heads",
             "f32": bench_pool(max(args.steps // 4, 3), 1, "f32", not args.no_cpu),
             "bf16": bench_pool(max(args.steps // 4, 3), 1, "bf16", not args.no_cpu)}
+        _pool_probe_fractions(extra["pool_codec"], extra.get("hbm_probe"))
     line = {
         "metric": METRIC,
         "value": value,

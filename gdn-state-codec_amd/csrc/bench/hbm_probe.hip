@@ -122,6 +122,9 @@ __global__ __launch_bounds__(kThreads) void write_kernel(uint4* __restrict__ dst
 //   expand   (1:4 read:write, the dequantize's mix): 16 KiB of bytes in, each
 //            byte widened to an fp32 value, 64 KiB out; a 4-byte load and a
 //            16-byte store per row.
+//   halve    (2:1, the bf16 pool encode's mix): 32 KiB of bf16 in, each
+//            value's low byte kept, 16 KiB out; an 8-byte load and a 4-byte
+//            store per row.
 //   contract (4:1, the quantize's mix): 64 KiB of fp32 in, each value's low
 //            byte kept, 16 KiB out; a 16-byte load and a 4-byte store per row.
 // Loads are all issued before the stores, as in the codec kernels.
@@ -174,6 +177,37 @@ __global__ __launch_bounds__(kThreads) void contract_kernel(const uint4* __restr
   for (int j = 0; j < kRowsPerThread; ++j) {
     const uint32_t packed = (v[j].x & 0xFFu) | ((v[j].y & 0xFFu) << 8) |
                             ((v[j].z & 0xFFu) << 16) | (v[j].w << 24);
+    uint32_t* q = out + (8 * j + row0) * (kTileDim / 4) + quad;
+    if (kNontemporal) {
+      __builtin_nontemporal_store(packed, q);
+    } else {
+      *q = packed;
+    }
+  }
+}
+
+template <bool kNontemporal, bool kXcd>
+__global__ __launch_bounds__(kThreads) void halve_kernel(const uint2* __restrict__ src,
+                                                         uint32_t* __restrict__ dst) {
+  const uint64_t tile = kXcd ? gdn::xcd_contiguous_item(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int row0 = threadIdx.x >> 5;
+  const int quad = threadIdx.x & 31;
+  const uint2* in = src + tile * (kTileDim * kTileDim / 4);
+  uint32_t* out = dst + tile * (kTileDim * kTileDim / 4);
+  uint2 v[kRowsPerThread];
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const uint2* p = in + (8 * j + row0) * (kTileDim / 4) + quad;
+    if constexpr (kNontemporal) {
+      v[j] = gdn::stream_load(p);
+    } else {
+      v[j] = *p;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const uint32_t packed = (v[j].x & 0xFFu) | (((v[j].x >> 16) & 0xFFu) << 8) |
+                            ((v[j].y & 0xFFu) << 16) | ((v[j].y >> 16) << 24);
     uint32_t* q = out + (8 * j + row0) * (kTileDim / 4) + quad;
     if (kNontemporal) {
       __builtin_nontemporal_store(packed, q);
@@ -296,6 +330,20 @@ extern "C" int32_t gdn_hbm_probe_contract(void* stream, const void* src, void* d
   const auto kernel = mode == 0 ? contract_kernel<false, false> : mode == 1 ? contract_kernel<true, false> : mode == 2 ? contract_kernel<false, true> : contract_kernel<true, true>;
   hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint4*>(src),
+                     static_cast<uint32_t*>(dst));
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+// 2:1 stream: `tiles` 32 KiB tiles of bf16 at src narrowed into `tiles` 16 KiB
+// tiles at dst (one workgroup per tile).
+extern "C" int32_t gdn_hbm_probe_halve(void* stream, const void* src, void* dst,
+                                       uint64_t tiles, uint32_t mode) {
+  if (src == nullptr || dst == nullptr || tiles == 0 || tiles > 0x7FFFFFFFull || mode > 3) {
+    return 1;
+  }
+  const auto kernel = mode == 0 ? halve_kernel<false, false> : mode == 1 ? halve_kernel<true, false> : mode == 2 ? halve_kernel<false, true> : halve_kernel<true, true>;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint2*>(src),
                      static_cast<uint32_t*>(dst));
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }

@@ -170,6 +170,38 @@ __device__ __forceinline__ float load_rows(const uint16_t* tile, uint32_t offset
   return key == 0u ? INFINITY : __uint_as_float(((0x10000u - key) >> 1) << 16);
 }
 
+// bf16 tiles in the [value][key] layout (the slot pool's) stay packed through
+// the encode (32 VGPRs for the thread's 64 values instead of 64): each phase
+// widens a value where it reads it, and the codes come from the input by the
+// certified direct lift.  The kernel then needs 124 VGPRs instead of 155, so 4
+// workgroups per CU instead of 3: config-5 bf16 gather-encode 4.25 -> 4.11 ms
+// in an A/B run, bit-identical.  In [key][value] the packed form needs 130
+// VGPRs (no gain in residency) and its extra VALU made it slower (4.34 ->
+// 4.54 ms), so that layout keeps the widened tile.
+__device__ __forceinline__ float load_rows_packed(const uint16_t* tile, uint32_t offset,
+                                                  uint2 (&raw)[kRowsPerThread]) {
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    raw[j] = stream_load(reinterpret_cast<const uint2*>(tile + offset + j * 8 * kDim));
+  }
+  u16x2_t multiplier = {0xFFFEu, 0xFFFEu};
+  asm("" : "+v"(multiplier));
+  u16x2_t best = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    best = __builtin_elementwise_max(best, __builtin_bit_cast(u16x2_t, raw[j].x) * multiplier);
+    best = __builtin_elementwise_max(best, __builtin_bit_cast(u16x2_t, raw[j].y) * multiplier);
+  }
+  const uint32_t key = max(static_cast<uint32_t>(best.x), static_cast<uint32_t>(best.y));
+  return key == 0u ? INFINITY : __uint_as_float(((0x10000u - key) >> 1) << 16);
+}
+
+// Value i (column 4 * c4 + i) of a packed row, widened to fp32 (exact).
+__device__ __forceinline__ float widen(const uint2& row, int i) {
+  const uint32_t word = i < 2 ? row.x : row.y;
+  return __uint_as_float((i & 1) == 0 ? word << 16 : word & 0xFFFF0000u);
+}
+
 // Cross-lane exchanges.  Encodes of bf16 tiles (the slot pool's) exchange on
 // the VALU (DPP and permlane swaps, lane_exchange.h); fp32 tiles go through
 // ds_bpermute (__shfl_xor).  Measured on one box against the all-bpermute
@@ -426,6 +458,121 @@ __device__ __forceinline__ void smooth_and_max(float (&x)[kRowsPerThread][4],
   }
 }
 
+// Packed bf16 tiles, phase 2: the per-value maxima of |m|, m = r / s, without
+// keeping m (the code phase forms its codes from r again).  Same maxima and
+// the same reductions as smooth_and_max.
+template <uint32_t kLayout, bool kFast, bool kValu>
+__device__ __forceinline__ void max_of_quotients(const uint2 (&raw)[kRowsPerThread],
+                                                 const float* s_shared,
+                                                 const float* s_inverse, int group,
+                                                 int c4, float (&mx)[kRowsPerThread]) {
+  if constexpr (kLayout == kKeyValue) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx[i] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+      const int key = 8 * j + group;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float r = widen(raw[j], i);
+        const float m = kFast ? div_by_reciprocal(r, s_shared[key], s_inverse[key])
+                              : r / s_shared[key];
+        mx[i] = max_abs<kFast>(mx[i], m);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+      float m[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = 4 * c4 + i;
+        const float r = widen(raw[j], i);
+        m[i] = kFast ? div_by_reciprocal(r, s_shared[key], s_inverse[key]) : r / s_shared[key];
+      }
+      mx[j] = max_abs<kFast>(max_abs<kFast>(m[0], m[1]), max_abs<kFast>(m[2], m[3]));
+    }
+    if constexpr (kFast) {
+      reduce_rows_over_half_wave<kValu>(mx, c4, FiniteMaxOp{});
+    } else {
+      reduce_rows_over_half_wave<kValu>(mx, c4, MaxOp{});
+    }
+  }
+}
+
+// Packed bf16 tiles, phase 3 on the fast domains (fast_divide and fast_scale):
+// codes from r by the certified direct lift (wide_code_lift, codec_math.h);
+// a row of four values whose smallest lift fraction is below its margin is
+// recomputed exactly, m = r / s and then m / scale by the reciprocal division.
+template <uint32_t kLayout>
+__device__ __forceinline__ void write_codes_wide(const uint2 (&raw)[kRowsPerThread],
+                                                 const float* s_shared, const float* s_inverse,
+                                                 const float* scale_shared,
+                                                 const float* scale_inverse,
+                                                 const float* code_factor, int group, int c4,
+                                                 int8_t* out) {
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    float lift[4];
+    float fraction[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
+      const int value = kLayout == kKeyValue ? 4 * c4 + i : 8 * j + group;
+      lift[i] = wide_code_lift(widen(raw[j], i), s_inverse[key], code_factor[value]);
+      fraction[i] = lift_fraction(lift[i]);
+    }
+    uint32_t packed = pack_lifted_codes(lift);
+    if (fminf(fminf(fraction[0], fraction[1]), fminf(fraction[2], fraction[3])) <
+        kWideLiftMargin) {
+      packed = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
+        const int value = kLayout == kKeyValue ? 4 * c4 + i : 8 * j + group;
+        const float m = div_by_reciprocal(widen(raw[j], i), s_shared[key], s_inverse[key]);
+        const float q = div_by_reciprocal(m, scale_shared[value], scale_inverse[value]);
+        const int code = round_half_away_small(q * kQuantizedMaximum);
+        packed |= (static_cast<uint32_t>(code) & 0xFFu) << (8 * i);
+      }
+    }
+    const uint32_t offset = static_cast<uint32_t>((8 * j + group) * kDim + 4 * c4);
+    stream_store(reinterpret_cast<uint32_t*>(out + offset), packed);
+  }
+}
+
+// Packed bf16 tiles, phase 3 off the fast domains: m = r / s by IEEE division
+// (what both of phase 2's divisions give), then write_codes' rounding.
+template <uint32_t kLayout, bool kFastScale>
+__device__ __forceinline__ void write_codes_packed(const uint2 (&raw)[kRowsPerThread],
+                                                   const float* s_shared,
+                                                   const float* scale_shared,
+                                                   const float* scale_inverse, int group,
+                                                   int c4, int8_t* out) {
+  // Fully unrolled: a rolled loop indexes raw[] at run time, which moves the
+  // whole array to scratch memory for every path of the kernel.
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
+      const int value = kLayout == kKeyValue ? 4 * c4 + i : 8 * j + group;
+      const float m = widen(raw[j], i) / s_shared[key];
+      const float scale = scale_shared[value];
+      float q;
+      if constexpr (kFastScale) {
+        q = div_by_reciprocal(m, scale, scale_inverse[value]);
+      } else {
+        q = scale == 0.0f ? 0.0f : m / scale;
+      }
+      const int code = round_half_away_small(q * kQuantizedMaximum);
+      packed |= (static_cast<uint32_t>(code) & 0xFFu) << (8 * i);
+    }
+    stream_store(reinterpret_cast<uint32_t*>(out + (8 * j + group) * kDim + 4 * c4), packed);
+  }
+}
+
 template <uint32_t kLayout, typename In, int kMode>
 __global__ __launch_bounds__(kThreads) void encode_kernel(
     const In* __restrict__ source, int8_t* __restrict__ codes,
@@ -458,8 +605,25 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   // nothing to a key sum and divide exactly on both division paths, so they
   // must not force the slow paths (dequantized states hold many exact zeros,
   // one per code 0).
-  float x[kRowsPerThread][4];
-  float min_abs = load_rows(tile, static_cast<uint32_t>(group * kDim + 4 * c4), x);
+  // Tiles are held widened in x (m = r / s replaces them in place), except
+  // bf16 tiles in [value][key], which stay packed in raw and are widened
+  // where read.
+  constexpr bool kPacked = sizeof(In) == 2 && kLayout == kValueKey;
+  float x[kPacked ? 1 : kRowsPerThread][4];
+  uint2 raw[kPacked ? kRowsPerThread : 1];
+  float min_abs;
+  if constexpr (kPacked) {
+    min_abs = load_rows_packed(tile, static_cast<uint32_t>(group * kDim + 4 * c4), raw);
+  } else {
+    min_abs = load_rows(tile, static_cast<uint32_t>(group * kDim + 4 * c4), x);
+  }
+  const auto input = [&](int j, int i) -> float {
+    if constexpr (kPacked) {
+      return widen(raw[j], i);
+    } else {
+      return x[j][i];
+    }
+  };
 
   bool fast_divide = false;
   if constexpr (kMode != kModeGivenSmoothing) {
@@ -468,10 +632,10 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
       double p[kRowsPerThread];
 #pragma unroll
       for (int j = 0; j < kRowsPerThread; ++j) {
-        p[j] = (static_cast<double>(fabsf(x[j][0])) +
-                static_cast<double>(fabsf(x[j][1]))) +
-               (static_cast<double>(fabsf(x[j][2])) +
-                static_cast<double>(fabsf(x[j][3])));
+        p[j] = (static_cast<double>(fabsf(input(j, 0))) +
+                static_cast<double>(fabsf(input(j, 1)))) +
+               (static_cast<double>(fabsf(input(j, 2))) +
+                static_cast<double>(fabsf(input(j, 3))));
       }
       reduce_rows_over_half_wave<kValu>(p, c4, AddOp{});
       if ((c4 & 1) == 0) key_sum[8 * ((c4 >> 1) & 15) + group] = p[0];
@@ -482,7 +646,7 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
         double acc = 0.0;
 #pragma unroll
         for (int j = 0; j < kRowsPerThread; ++j) {
-          acc += static_cast<double>(fabsf(x[j][i]));
+          acc += static_cast<double>(fabsf(input(j, i)));
         }
         p[i] = with_partner<kValu, 32>(acc, AddOp{});
       }
@@ -551,10 +715,18 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   // ---- m = r / s and the per-value scales max |m| over keys ----------------
   // The branch is uniform over the workgroup; each side is straight-line code.
   float mx[kRowsPerThread];
-  if (fast_divide) {
-    smooth_and_max<kLayout, true, kValu>(x, s_shared, s_inverse, group, c4, mx);
+  if constexpr (kPacked) {
+    if (fast_divide) {
+      max_of_quotients<kLayout, true, kValu>(raw, s_shared, s_inverse, group, c4, mx);
+    } else {
+      max_of_quotients<kLayout, false, kValu>(raw, s_shared, s_inverse, group, c4, mx);
+    }
   } else {
-    smooth_and_max<kLayout, false, kValu>(x, s_shared, s_inverse, group, c4, mx);
+    if (fast_divide) {
+      smooth_and_max<kLayout, true, kValu>(x, s_shared, s_inverse, group, c4, mx);
+    } else {
+      smooth_and_max<kLayout, false, kValu>(x, s_shared, s_inverse, group, c4, mx);
+    }
   }
   if constexpr (kLayout == kKeyValue) {
 #pragma unroll
@@ -587,7 +759,18 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
 
   // ---- codes ---------------------------------------------------------------
   int8_t* out = codes + item * kTile;
-  if (fast_scale && fast_divide) {  // m finite: every r / s took the fast division
+  if constexpr (kPacked) {
+    if (fast_scale && fast_divide) {
+      write_codes_wide<kLayout>(raw, s_shared, s_inverse, scale_shared, scale_inverse,
+                                code_factor, group, c4, out);
+    } else if (fast_scale) {
+      write_codes_packed<kLayout, true>(raw, s_shared, scale_shared, scale_inverse, group, c4,
+                                        out);
+    } else {
+      write_codes_packed<kLayout, false>(raw, s_shared, scale_shared, scale_inverse, group, c4,
+                                         out);
+    }
+  } else if (fast_scale && fast_divide) {  // m finite: every r / s took the fast division
     write_codes_lifted<kLayout>(x, scale_shared, scale_inverse, code_factor, group, c4, out);
   } else if (fast_scale) {
     write_codes<kLayout, true>(x, scale_shared, scale_inverse, group, c4, out);

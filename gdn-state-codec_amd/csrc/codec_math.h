@@ -89,6 +89,25 @@ constexpr float kCodeLiftMargin = 0x1p-13f;
 
 GDN_HD float code_lift(float m, float factor) { return fmaf(m, factor, kCodeLiftOffset); }
 
+// The same code formed from the stage's input r instead of m = RN(r / s), for
+// an encoder that does not keep m: u = RN(RN(r * y) * factor + 0.5 + 2^-13)
+// with y = RN(1 / s) and factor = RN(127 / scale).  Preconditions: m = RN(r / s)
+// satisfies |m| <= scale, r * y and r / s are 0 or normal, factor as above.
+// With A = r / s, p = RN(RN(m / scale) * 127) = 127 A / scale (1+d0)(1+d1)(1+d2)
+// and Y = RN(r * y) * factor = 127 A / scale (1+e1)(1+e2)(1+e3), all |di|, |ei|
+// <= 2^-24, and |A / scale| <= 1 + 2^-24, so |p - Y| <= 127 * 6.01 * 2^-24 <
+// 2^-14.4; the lift's rounding adds at most 2^-18, so p + 0.5 lies within
+// 2^-14.3 of u - 2^-13.  If fract(u) >= 2^-12, p + 0.5 lies strictly between
+// floor(u) and floor(u) + 1 (2^-12 - 2^-13 > 2^-14.3 on the low side, 2^-13 >
+// 2^-14.3 on the high side): no tie, and lround(p) = floor(u).  Values with
+// fract(u) < 2^-12 (about 1 in 4,096) take the exact path.
+constexpr float kWideLiftOffset = 0.5f + 0x1p-13f;
+constexpr float kWideLiftMargin = 0x1p-12f;
+
+GDN_HD float wide_code_lift(float r, float reciprocal, float factor) {
+  return fmaf(r * reciprocal, factor, kWideLiftOffset);
+}
+
 // x - floor(x); on the device one v_fract_f32 (which returns the largest float
 // below 1 where the subtraction would round to 1; both compare >= the margin).
 GDN_HD float lift_fraction(float u) {

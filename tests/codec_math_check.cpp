@@ -28,6 +28,15 @@
 //   codec_math_check lift_refit      the same sweep against the refit re-encode's
 //                                    rounding, trunc(RN(q +- 0.5)) clamped to +-127
 //                                    (window_boundary.cpp:336-345)
+//   codec_math_check wide_lift       the bf16 encoder's codes from its input r:
+//                                    wherever lift_fraction(wide_code_lift(r,
+//                                    RN(1/s), RN(127/scale))) >= kWideLiftMargin,
+//                                    its floor is clamp(lround(RN(RN(RN(r/s)/scale)
+//                                    *127)), -127, 127); 16,384 random (s, scale)
+//                                    pairs over the fast domains, scale the
+//                                    quotient of a random bf16 maximum, times every
+//                                    bf16 r with |RN(r/s)| <= scale.  The count of
+//                                    values left to the exact path goes to stderr.
 //   codec_math_check order           xcd_contiguous_item (work_order.h) is a
 //                                    bijection on 0 .. n-1 for every n up to
 //                                    4096 and for the bench grids
@@ -39,6 +48,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <cmath>
 #include <thread>
 #include <vector>
 
@@ -272,6 +282,49 @@ void check_lift() {
   fprintf(stderr, "fallbacks %llu\n", static_cast<unsigned long long>(lift_fallbacks.load()));
 }
 
+// The bf16 encoder's direct lift (codec_math.h, wide_code_lift) against the
+// reference chain on every bf16 input of random (s, scale) pairs.  s is drawn
+// over [2^-14, 2^20] (the smoothing's fast-division domain; s >= sqrt(1e-8)),
+// the scale is |RN(R / s)| for a random bf16 R chosen so that it lies in
+// [2^-90, 2^90], and r runs over every finite bf16 with |r| >= 2^-100 or
+// r = 0 and |RN(r / s)| <= scale, as in a tile whose maximum is R.
+void check_wide_lift() {
+  std::atomic<uint64_t> fallbacks{0};
+  parallel(0, 16384, [&](uint64_t d, uint64_t& n, uint64_t& bad) {
+    uint64_t state = 0xD1B54A32D192ED03ULL * (d + 7);
+    const uint32_t s_exp = 127 - 14 + random_u32(state) % 35;
+    const float s = from_bits((s_exp << 23) | (random_u32(state) & 0x7FFFFFu));
+    const float y = 1.0f / s;
+    float scale = 0.0f;
+    while (!(scale >= 0x1p-90f && scale <= 0x1p90f)) {
+      const uint32_t r_exp = 127 - 100 + random_u32(state) % 200;
+      const float big = from_bits((r_exp << 23) | ((random_u32(state) & 0x7Fu) << 16));
+      scale = fabsf(big / s);
+    }
+    const float factor = gdn::kQuantizedMaximum / scale;
+    uint64_t fb = 0;
+    for (uint32_t h = 0; h < 0x10000u; ++h) {
+      const float r = from_bits(h << 16);
+      if (!std::isfinite(r) || (r != 0.0f && fabsf(r) < 0x1p-100f)) continue;
+      const float m = r / s;
+      if (!(fabsf(m) <= scale)) continue;
+      ++n;
+      const float u = gdn::wide_code_lift(r, y, factor);
+      if (!(gdn::lift_fraction(u) >= gdn::kWideLiftMargin)) {
+        ++fb;
+        continue;
+      }
+      const float q = m / scale;
+      long expect = lroundf(q * gdn::kQuantizedMaximum);
+      if (expect < -127) expect = -127;
+      if (expect > 127) expect = 127;
+      if (gdn::lifted_code(u) != expect) ++bad;
+    }
+    fallbacks += fb;
+  });
+  fprintf(stderr, "fallbacks %llu\n", static_cast<unsigned long long>(fallbacks.load()));
+}
+
 void check_order_grid(uint64_t blocks) {
   std::vector<uint8_t> seen(blocks, 0);
   bool ok = true;
@@ -311,6 +364,8 @@ int main(int argc, char** argv) {
     check_round();
   } else if (strcmp(argv[1], "lift") == 0) {
     check_lift();
+  } else if (strcmp(argv[1], "wide_lift") == 0) {
+    check_wide_lift();
   } else if (strcmp(argv[1], "lift_refit") == 0) {
     refit_rounding = true;
     check_lift();

@@ -89,6 +89,17 @@ def test_lifted_codes_match_the_refit_rounding_wherever_the_margin_admits_them(c
     assert checked > 3_000_000_000 and failures == 0 and rc == 0
 
 
+def test_bf16_direct_lift_matches_lround_wherever_its_margin_admits_it(checker):
+    """The bf16 pool encoder's codes formed from the input r without keeping
+    m = r / s (wide_code_lift in codec_math.h) against clamp(lround(RN(RN(RN(r/s)
+    / scale) * 127))) in IEEE fp32: every bf16 r of 16,384 random (s, scale)
+    pairs over the fast domains.  With the margin lowered to 2^-20, or the
+    offset to 0.5, this check fails (thousands of mismatches), so the margin
+    and the offset are what make it pass."""
+    rc, checked, failures = _run(checker, "wide_lift")
+    assert checked > 400_000_000 and failures == 0 and rc == 0
+
+
 def test_xcd_contiguous_order_is_a_bijection(checker):
     """The streaming kernels' workgroup -> tile order (csrc/work_order.h) visits
     every tile exactly once for every grid size up to 4,096 and the bench's."""

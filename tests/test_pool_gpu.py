@@ -62,6 +62,42 @@ def test_pool_encode_decode_match_oracle(device, bf16, layout):
     assert (got[:, untouched] == poison[:, untouched]).all()
 
 
+@pytest.mark.parametrize("layout", [KV, VK])
+@pytest.mark.parametrize("kind", ["c1", "student_t", "wide", "tiny_and_huge", "zeros",
+                                  "requantize"])
+def test_bf16_pool_encode_edge_cases_match_oracle(device, layout, kind):
+    """bf16 tiles are encoded from their packed form: the codes on the fast
+    domains come from the input directly (the certified lift of codec_math.h),
+    with the exact path for values inside its margin, and the IEEE paths for
+    tiles outside the fast domains (subnormal and 1e30-scale entries).  Every
+    kind of tile the fp32 parity test uses, rounded to bf16, bit-exact."""
+    print(f"bf16 pool edge cases layout={layout} kind={kind}", flush=True)
+    if kind == "c1":
+        x = datagen.c1_heads(64, 15)
+    elif kind == "student_t":
+        x = datagen.student_t_heads(64, 16, zero_fraction=0.05)
+    elif kind == "wide":
+        x = np.stack([datagen.wide_range_head(400 + i) for i in range(24)])
+    elif kind == "tiny_and_huge":
+        x = np.stack([datagen.tiny_head(500 + i) for i in range(12)]
+                     + [datagen.huge_head(600 + i) for i in range(12)])
+    elif kind == "zeros":
+        x = np.stack([datagen.zero_rows_cols_head(700 + i) for i in range(16)])
+    else:
+        # Re-encoded dequantized states: exact zeros, half of them -0.
+        x = datagen.student_t_heads(48, 17)
+        x = oracle.decode_heads(*oracle.encode_heads(x, layout, threads=8), layout, threads=8)
+        zeros = np.flatnonzero(x == 0)
+        x.reshape(-1)[zeros[::2]] = -0.0
+    pool = oracle.f32_to_bf16(x).reshape((1, x.shape[0], 1, 128, 128))
+    ids = np.arange(x.shape[0], dtype=np.int32)[::-1].copy()
+    oc, os, osc = oracle.pool_encode(pool, ids, layout, threads=8)
+    c, s, sc = codec.pool_encode(_as_torch(pool, device), torch.from_numpy(ids).to(device), layout)
+    assert to_np(c).tobytes() == oc.tobytes()
+    assert to_np(s).tobytes() == os.tobytes()
+    assert to_np(sc).tobytes() == osc.tobytes()
+
+
 def test_out_of_range_slot_ids_are_skipped(device):
     pool = _pool(1, 4, 2, 92, False)
     ids = np.array([0, 4, 1000, -5, 3], np.int32)  # 4 and 1000 are >= slots
