@@ -53,7 +53,9 @@ int32_t statecentric_gdn_state_codec_encoded_projection_decode_launch_v4(
  * outputs [seqs][tokens][value_heads][128] fp32.  The reference has no such
  * entry point (its prefill runs the dense chunk_gated_delta_rule,
  * src/gdn_state_codec/host_gdn.py:305-344); this is the same readout applied
- * to every token. */
+ * to every token.  Returns 1 as well when one sequence's output rows span
+ * 2^32 bytes or more (tokens * value_heads * 512 >= 2^32): the kernel
+ * addresses them with 32-bit offsets from a per-sequence base. */
 int32_t statecentric_gdn_state_codec_encoded_projection_chunked_launch_v4(
     void* stream, const int8_t* residual, const float* smoothing,
     const float* value_scales, const uint16_t* queries, float* outputs,
