@@ -779,22 +779,18 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   }
 }
 
-// Decode thread layouts.  kWaves wavefronts per tile; a lane handles rows
-// row(j) of the tile, j = 0 .. 64 / kWaves - 1, and the four columns
-// 4*(lane%32)..+3, so every store instruction writes two whole rows of
-// contiguous HBM.  With g = thread / 32:
-//   interleaved: row(j) = 2 kWaves j + g (the wavefronts advance together);
-//   bands:       row(j) = (128 / kWaves)(g / 2) + 2j + g % 2 (each wavefront
-//                writes its own contiguous band of 128 / kWaves rows).
-template <int kWaves, bool kBands>
+// Decode thread layout: kWaves wavefronts per tile, interleaved.  A lane
+// handles rows 2 kWaves j + t / 32 of the tile, j = 0 .. 64 / kWaves - 1, and
+// the four columns 4*(t%32)..+3, so every store instruction writes two whole
+// rows of contiguous HBM and the wavefronts advance through the tile together.
+// (Each wavefront writing its own contiguous band of rows measured slower; see
+// launch_decode.)
+template <int kWaves>
 struct DecodeShape {
   static constexpr int kThreadCount = 64 * kWaves;
   static constexpr int kRows = 64 / kWaves;  // rows per thread
-  __device__ static int first_row(int t) {
-    const int g = t >> 5;
-    return kBands ? (kDim / kWaves) * (g >> 1) + (g & 1) : g;
-  }
-  static constexpr int kRowStep = kBands ? 2 : 2 * kWaves;
+  static constexpr int kRowStep = 2 * kWaves;
+  __device__ static int first_row(int t) { return t >> 5; }
 };
 
 // dense = ((s[k] * code) / 127) * scale[v] (+ sum_r ck[k][r] * cv[v][r]) for
@@ -922,32 +918,18 @@ int32_t launch_encode(void* stream, const void* source, uint32_t dtype,
                       map);
 }
 
-template <bool kCompensated, typename Shape>
+template <bool kCompensated, typename Shape, typename Out>
 int32_t launch_decode_shaped(void* stream, const int8_t* codes, const float* smoothing,
                              const float* scales, const float* compensator_keys,
-                             const float* compensator_values, void* dense,
-                             uint32_t dtype, uint64_t items, uint32_t layout,
-                             TileMap map) {
+                             const float* compensator_values, Out* dense, uint64_t items,
+                             uint32_t layout, TileMap map) {
   const dim3 grid(static_cast<uint32_t>(items));
   const dim3 block(Shape::kThreadCount);
-  if (dtype == kDtypeF32) {
-    float* dst = static_cast<float*>(dense);
-    return layout == kKeyValue
-               ? launch(decode_kernel<kKeyValue, float, kCompensated, Shape>, grid,
-                        block, stream, codes, smoothing, scales,
-                        compensator_keys, compensator_values, dst, map)
-               : launch(decode_kernel<kValueKey, float, kCompensated, Shape>, grid,
-                        block, stream, codes, smoothing, scales,
-                        compensator_keys, compensator_values, dst, map);
-  }
-  uint16_t* dst = static_cast<uint16_t*>(dense);
   return layout == kKeyValue
-             ? launch(decode_kernel<kKeyValue, uint16_t, kCompensated, Shape>, grid,
-                      block, stream, codes, smoothing, scales,
-                      compensator_keys, compensator_values, dst, map)
-             : launch(decode_kernel<kValueKey, uint16_t, kCompensated, Shape>, grid,
-                      block, stream, codes, smoothing, scales,
-                      compensator_keys, compensator_values, dst, map);
+             ? launch(decode_kernel<kKeyValue, Out, kCompensated, Shape>, grid, block, stream,
+                      codes, smoothing, scales, compensator_keys, compensator_values, dense, map)
+             : launch(decode_kernel<kValueKey, Out, kCompensated, Shape>, grid, block, stream,
+                      codes, smoothing, scales, compensator_keys, compensator_values, dense, map);
 }
 
 // Thread layout per output type, from A/B runs on one box (ms, bit-identical;
@@ -969,12 +951,12 @@ int32_t launch_decode(void* stream, const int8_t* codes, const float* smoothing,
                       uint32_t dtype, uint64_t items, uint32_t layout,
                       TileMap map) {
   return dtype == kDtypeF32
-             ? launch_decode_shaped<kCompensated, DecodeShape<16, false>>(
+             ? launch_decode_shaped<kCompensated, DecodeShape<16>>(
                    stream, codes, smoothing, scales, compensator_keys, compensator_values,
-                   dense, dtype, items, layout, map)
-             : launch_decode_shaped<kCompensated, DecodeShape<8, false>>(
+                   static_cast<float*>(dense), items, layout, map)
+             : launch_decode_shaped<kCompensated, DecodeShape<8>>(
                    stream, codes, smoothing, scales, compensator_keys, compensator_values,
-                   dense, dtype, items, layout, map);
+                   static_cast<uint16_t*>(dense), items, layout, map);
 }
 
 constexpr TileMap kIdentityMap{nullptr, 0, 0, 0, false};
