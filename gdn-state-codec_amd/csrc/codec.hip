@@ -149,10 +149,14 @@ typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float load_rows(const uint16_t* tile, uint32_t offset,
                                            float (&x)[kRowsPerThread][4]) {
+  // 32-bit byte offsets from the workgroup's tile base: the loads use the
+  // scalar-base addressing form instead of a 64-bit address per row.
+  const char* base = reinterpret_cast<const char*>(tile);
   uint2 raw[kRowsPerThread];
 #pragma unroll
   for (int j = 0; j < kRowsPerThread; ++j) {
-    raw[j] = stream_load(reinterpret_cast<const uint2*>(tile + offset + j * 8 * kDim));
+    const uint32_t bytes = 2u * (offset + static_cast<uint32_t>(j * 8 * kDim));
+    raw[j] = stream_load(reinterpret_cast<const uint2*>(base + bytes));
   }
   u16x2_t multiplier = {0xFFFEu, 0xFFFEu};
   asm("" : "+v"(multiplier));
@@ -168,38 +172,6 @@ __device__ __forceinline__ float load_rows(const uint16_t* tile, uint32_t offset
   }
   const uint32_t key = max(static_cast<uint32_t>(best.x), static_cast<uint32_t>(best.y));
   return key == 0u ? INFINITY : __uint_as_float(((0x10000u - key) >> 1) << 16);
-}
-
-// bf16 tiles in the [value][key] layout (the slot pool's) stay packed through
-// the encode (32 VGPRs for the thread's 64 values instead of 64): each phase
-// widens a value where it reads it, and the codes come from the input by the
-// certified direct lift.  The kernel then needs 124 VGPRs instead of 155, so 4
-// workgroups per CU instead of 3: config-5 bf16 gather-encode 4.25 -> 4.11 ms
-// in an A/B run, bit-identical.  In [key][value] the packed form needs 130
-// VGPRs (no gain in residency) and its extra VALU made it slower (4.34 ->
-// 4.54 ms), so that layout keeps the widened tile.
-__device__ __forceinline__ float load_rows_packed(const uint16_t* tile, uint32_t offset,
-                                                  uint2 (&raw)[kRowsPerThread]) {
-#pragma unroll
-  for (int j = 0; j < kRowsPerThread; ++j) {
-    raw[j] = stream_load(reinterpret_cast<const uint2*>(tile + offset + j * 8 * kDim));
-  }
-  u16x2_t multiplier = {0xFFFEu, 0xFFFEu};
-  asm("" : "+v"(multiplier));
-  u16x2_t best = {0u, 0u};
-#pragma unroll
-  for (int j = 0; j < kRowsPerThread; ++j) {
-    best = __builtin_elementwise_max(best, __builtin_bit_cast(u16x2_t, raw[j].x) * multiplier);
-    best = __builtin_elementwise_max(best, __builtin_bit_cast(u16x2_t, raw[j].y) * multiplier);
-  }
-  const uint32_t key = max(static_cast<uint32_t>(best.x), static_cast<uint32_t>(best.y));
-  return key == 0u ? INFINITY : __uint_as_float(((0x10000u - key) >> 1) << 16);
-}
-
-// Value i (column 4 * c4 + i) of a packed row, widened to fp32 (exact).
-__device__ __forceinline__ float widen(const uint2& row, int i) {
-  const uint32_t word = i < 2 ? row.x : row.y;
-  return __uint_as_float((i & 1) == 0 ? word << 16 : word & 0xFFFF0000u);
 }
 
 // Cross-lane exchanges.  Encodes of bf16 tiles (the slot pool's) exchange on
@@ -458,68 +430,60 @@ __device__ __forceinline__ void smooth_and_max(float (&x)[kRowsPerThread][4],
   }
 }
 
-// Packed bf16 tiles, phase 2: the per-value maxima of |m|, m = r / s, without
-// keeping m (the code phase forms its codes from r again).  Same maxima and
-// the same reductions as smooth_and_max.
-template <uint32_t kLayout, bool kFast, bool kValu>
-__device__ __forceinline__ void max_of_quotients(const uint2 (&raw)[kRowsPerThread],
-                                                 const float* s_shared,
-                                                 const float* s_inverse, int group,
-                                                 int c4, float (&mx)[kRowsPerThread]) {
-  if constexpr (kLayout == kKeyValue) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mx[i] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j) {
-      const int key = 8 * j + group;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float r = widen(raw[j], i);
-        const float m = kFast ? div_by_reciprocal(r, s_shared[key], s_inverse[key])
-                              : r / s_shared[key];
-        mx[i] = max_abs<kFast>(mx[i], m);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j) {
-      float m[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = 4 * c4 + i;
-        const float r = widen(raw[j], i);
-        m[i] = kFast ? div_by_reciprocal(r, s_shared[key], s_inverse[key]) : r / s_shared[key];
-      }
-      mx[j] = max_abs<kFast>(max_abs<kFast>(m[0], m[1]), max_abs<kFast>(m[2], m[3]));
-    }
-    if constexpr (kFast) {
-      reduce_rows_over_half_wave<kValu>(mx, c4, FiniteMaxOp{});
-    } else {
-      reduce_rows_over_half_wave<kValu>(mx, c4, MaxOp{});
-    }
-  }
-}
+// bf16 tiles in the [value][key] layout (the slot pool's) keep, on the fast
+// domains, the product q0 = RN(r * RN(1/s)) in place of r: it is the first step
+// of the reciprocal division of phase 2 and the operand of the code phase's
+// lift (wide_code_lift, codec_math.h), which then needs one fma per value.  The
+// exact path recovers r from q0 (bf16_input_from_product).  In [key][value] and
+// for fp32 tiles phase 2 keeps m = r / s instead.
+template <typename In, uint32_t kLayout>
+constexpr bool kKeepsProduct = sizeof(In) == 2 && kLayout == kValueKey;
 
-// Packed bf16 tiles, phase 3 on the fast domains (fast_divide and fast_scale):
-// codes from r by the certified direct lift (wide_code_lift, codec_math.h);
-// a row of four values whose smallest lift fraction is below its margin is
-// recomputed exactly, m = r / s and then m / scale by the reciprocal division.
-template <uint32_t kLayout>
-__device__ __forceinline__ void write_codes_wide(const uint2 (&raw)[kRowsPerThread],
-                                                 const float* s_shared, const float* s_inverse,
-                                                 const float* scale_shared,
-                                                 const float* scale_inverse,
-                                                 const float* code_factor, int group, int c4,
-                                                 int8_t* out) {
+// Phase 2 on the fast domain for kKeepsProduct tiles: x becomes q0; the row
+// maxima are those of m = RN(r / s), completed from q0 by the division's two
+// remaining steps, with the same reductions as smooth_and_max.
+template <bool kValu>
+__device__ __forceinline__ void products_and_max(float (&x)[kRowsPerThread][4],
+                                                 const float* s_shared,
+                                                 const float* s_inverse, int c4,
+                                                 float (&mx)[kRowsPerThread]) {
 #pragma unroll
   for (int j = 0; j < kRowsPerThread; ++j) {
+    float m[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = 4 * c4 + i;
+      const float q0 = x[j][i] * s_inverse[key];
+      m[i] = quotient_from_product(q0, x[j][i], s_shared[key], s_inverse[key]);
+      x[j][i] = q0;
+    }
+    mx[j] = max_abs<true>(max_abs<true>(m[0], m[1]), max_abs<true>(m[2], m[3]));
+  }
+  reduce_rows_over_half_wave<kValu>(mx, c4, FiniteMaxOp{});
+}
+
+// m = RN(r / s) of a kept product q0, with r recovered from it.
+__device__ __forceinline__ float quotient_of_kept_product(float q0, float s, float y) {
+  return quotient_from_product(q0, bf16_input_from_product(q0, s), s, y);
+}
+
+// Phase 3 for kKeepsProduct tiles on the fast domains: codes from q0 by the
+// direct lift; a row of four values whose smallest lift fraction is below the
+// margin is recomputed exactly (m from q0, then m / scale by the reciprocal
+// division and write_codes' rounding).
+__device__ __forceinline__ void write_codes_from_products(
+    const float (&x)[kRowsPerThread][4], const float* s_shared, const float* s_inverse,
+    const float* scale_shared, const float* scale_inverse, const float* code_factor,
+    int group, int c4, int8_t* out) {
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const int value = 8 * j + group;
+    const float factor = code_factor[value];
     float lift[4];
     float fraction[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
-      const int value = kLayout == kKeyValue ? 4 * c4 + i : 8 * j + group;
-      lift[i] = wide_code_lift(widen(raw[j], i), s_inverse[key], code_factor[value]);
+      lift[i] = wide_code_lift(x[j][i], factor);
       fraction[i] = lift_fraction(lift[i]);
     }
     uint32_t packed = pack_lifted_codes(lift);
@@ -528,40 +492,76 @@ __device__ __forceinline__ void write_codes_wide(const uint2 (&raw)[kRowsPerThre
       packed = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
-        const int value = kLayout == kKeyValue ? 4 * c4 + i : 8 * j + group;
-        const float m = div_by_reciprocal(widen(raw[j], i), s_shared[key], s_inverse[key]);
+        const int key = 4 * c4 + i;
+        const float m = quotient_of_kept_product(x[j][i], s_shared[key], s_inverse[key]);
         const float q = div_by_reciprocal(m, scale_shared[value], scale_inverse[value]);
         const int code = round_half_away_small(q * kQuantizedMaximum);
         packed |= (static_cast<uint32_t>(code) & 0xFFu) << (8 * i);
       }
     }
-    const uint32_t offset = static_cast<uint32_t>((8 * j + group) * kDim + 4 * c4);
+    const uint32_t offset = static_cast<uint32_t>(value * kDim + 4 * c4);
     stream_store(reinterpret_cast<uint32_t*>(out + offset), packed);
   }
 }
 
-// Packed bf16 tiles, phase 3 off the fast domains: m = r / s by IEEE division
-// (what both of phase 2's divisions give), then write_codes' rounding.
-template <uint32_t kLayout, bool kFastScale>
-__device__ __forceinline__ void write_codes_packed(const uint2 (&raw)[kRowsPerThread],
-                                                   const float* s_shared,
-                                                   const float* scale_shared,
-                                                   const float* scale_inverse, int group,
-                                                   int c4, int8_t* out) {
-  // Fully unrolled: a rolled loop indexes raw[] at run time, which moves the
-  // whole array to scratch memory for every path of the kernel.
+// kKeepsProduct tiles off the fast domains (tiles with a non-zero |r| below
+// 2^-100 or a key sum above 2^46, or a scale outside [2^-90, 2^90]; rare) read
+// their rows again from memory, one row at a time, and divide by IEEE
+// division: these paths hold no tile in registers, which leaves the fast path
+// its register budget (4 workgroups per CU).  Row j of the thread: values
+// 4*c4 .. 4*c4+3 of value row 8*j + group.
+__device__ __forceinline__ void reload_row(const uint16_t* tile, int group, int c4, int j,
+                                           float (&r)[4]) {
+  const uint32_t bytes = 2u * static_cast<uint32_t>((8 * j + group) * kDim + 4 * c4);
+  const uint2 raw =
+      stream_load(reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(tile) + bytes));
+  r[0] = __uint_as_float(raw.x << 16);
+  r[1] = __uint_as_float(raw.x & 0xFFFF0000u);
+  r[2] = __uint_as_float(raw.y << 16);
+  r[3] = __uint_as_float(raw.y & 0xFFFF0000u);
+}
+
+// Phase 2 off the fast domain: the row maxima of |r / s|, as smooth_and_max's
+// IEEE path forms them.
+template <bool kValu>
+__device__ __forceinline__ void reloaded_quotient_max(const uint16_t* tile,
+                                                      const float* s_shared, int group,
+                                                      int c4, float (&mx)[kRowsPerThread]) {
 #pragma unroll
   for (int j = 0; j < kRowsPerThread; ++j) {
+    float r[4];
+    reload_row(tile, group, c4, j, r);
+    float m[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m[i] = r[i] / s_shared[4 * c4 + i];
+    mx[j] = max_abs<false>(max_abs<false>(m[0], m[1]), max_abs<false>(m[2], m[3]));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  reduce_rows_over_half_wave<kValu>(mx, c4, MaxOp{});
+}
+
+// Phase 3 off the fast domains: m = r / s, then write_codes' division by the
+// scale (the reciprocal division when fast_scale) and rounding.  fast_scale is
+// a run-time argument: two instantiations on the two sides of a branch would
+// start with the same address arithmetic, which the compiler hoists above the
+// branch and keeps live for all 16 rows.
+__device__ __forceinline__ void write_codes_reloaded(const uint16_t* tile,
+                                                     const float* s_shared,
+                                                     const float* scale_shared,
+                                                     const float* scale_inverse, int group,
+                                                     int c4, int8_t* out, bool fast_scale) {
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const int value = 8 * j + group;
+    float r[4];
+    reload_row(tile, group, c4, j, r);
     uint32_t packed = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key = kLayout == kKeyValue ? 8 * j + group : 4 * c4 + i;
-      const int value = kLayout == kKeyValue ? 4 * c4 + i : 8 * j + group;
-      const float m = widen(raw[j], i) / s_shared[key];
+      const float m = r[i] / s_shared[4 * c4 + i];
       const float scale = scale_shared[value];
       float q;
-      if constexpr (kFastScale) {
+      if (fast_scale) {
         q = div_by_reciprocal(m, scale, scale_inverse[value]);
       } else {
         q = scale == 0.0f ? 0.0f : m / scale;
@@ -569,12 +569,42 @@ __device__ __forceinline__ void write_codes_packed(const uint2 (&raw)[kRowsPerTh
       const int code = round_half_away_small(q * kQuantizedMaximum);
       packed |= (static_cast<uint32_t>(code) & 0xFFu) << (8 * i);
     }
-    stream_store(reinterpret_cast<uint32_t*>(out + (8 * j + group) * kDim + 4 * c4), packed);
+    stream_store(reinterpret_cast<uint32_t*>(out + value * kDim + 4 * c4), packed);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
+// The scale step of encode_kernel for kKeepsProduct tiles ([value][key]): the
+// per-value scales from the row maxima of |m| (mx[0] of lanes with even c4,
+// as reduce_rows_over_half_wave leaves them), written to LDS with their
+// reciprocals and code factors, and to `scales`.  Returns, for the whole
+// workgroup, whether every scale is 0 or in [2^-90, 2^90] (fast_scale).  The
+// other tiles keep the step inline in encode_kernel: moved into a call, it
+// changed the code generated for the fp32 kernels.
+__device__ __forceinline__ bool finish_value_key_scales(const float (&mx)[kRowsPerThread],
+                                                        float* scale_shared,
+                                                        float* scale_inverse,
+                                                        float* code_factor, float* scales,
+                                                        int t, int group, int c4) {
+  if ((c4 & 1) == 0) scale_shared[8 * ((c4 >> 1) & 15) + group] = mx[0];
+  __syncthreads();
+  bool scale_ok = true;
+  if (t < kDim) {
+    const float scale = scale_shared[t];
+    scale_inverse[t] = scale == 0.0f ? 0.0f : 1.0f / scale;
+    code_factor[t] = scale == 0.0f ? 0.0f : kQuantizedMaximum / scale;
+    scales[t] = scale;
+    scale_ok = scale == 0.0f || (scale >= 0x1p-90f && scale <= 0x1p90f);
+  }
+  return __syncthreads_and(scale_ok) != 0;
+}
+
+// kKeepsProduct tiles are compiled for 4 wavefronts per SIMD (at most 128
+// VGPRs, 4 workgroups per CU); without the bound the allocator spreads the
+// kept products over 136.
 template <uint32_t kLayout, typename In, int kMode>
-__global__ __launch_bounds__(kThreads) void encode_kernel(
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(kKeepsProduct<In, kLayout> ? 4 : 1))) void encode_kernel(
     const In* __restrict__ source, int8_t* __restrict__ codes,
     float* __restrict__ smoothing, float* __restrict__ scales,
     const float* __restrict__ given_smoothing, TileMap map) {
@@ -605,25 +635,11 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   // nothing to a key sum and divide exactly on both division paths, so they
   // must not force the slow paths (dequantized states hold many exact zeros,
   // one per code 0).
-  // Tiles are held widened in x (m = r / s replaces them in place), except
-  // bf16 tiles in [value][key], which stay packed in raw and are widened
-  // where read.
-  constexpr bool kPacked = sizeof(In) == 2 && kLayout == kValueKey;
-  float x[kPacked ? 1 : kRowsPerThread][4];
-  uint2 raw[kPacked ? kRowsPerThread : 1];
-  float min_abs;
-  if constexpr (kPacked) {
-    min_abs = load_rows_packed(tile, static_cast<uint32_t>(group * kDim + 4 * c4), raw);
-  } else {
-    min_abs = load_rows(tile, static_cast<uint32_t>(group * kDim + 4 * c4), x);
-  }
-  const auto input = [&](int j, int i) -> float {
-    if constexpr (kPacked) {
-      return widen(raw[j], i);
-    } else {
-      return x[j][i];
-    }
-  };
+  // Tiles are held widened in x; phase 2 replaces r in place by m = r / s, or
+  // by q0 = RN(r * RN(1/s)) for kKeepsProduct tiles on the fast domain.
+  constexpr bool kKeepProduct = kKeepsProduct<In, kLayout>;
+  float x[kRowsPerThread][4];
+  float min_abs = load_rows(tile, static_cast<uint32_t>(group * kDim + 4 * c4), x);
 
   bool fast_divide = false;
   if constexpr (kMode != kModeGivenSmoothing) {
@@ -632,10 +648,8 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
       double p[kRowsPerThread];
 #pragma unroll
       for (int j = 0; j < kRowsPerThread; ++j) {
-        p[j] = (static_cast<double>(fabsf(input(j, 0))) +
-                static_cast<double>(fabsf(input(j, 1)))) +
-               (static_cast<double>(fabsf(input(j, 2))) +
-                static_cast<double>(fabsf(input(j, 3))));
+        p[j] = (static_cast<double>(fabsf(x[j][0])) + static_cast<double>(fabsf(x[j][1]))) +
+               (static_cast<double>(fabsf(x[j][2])) + static_cast<double>(fabsf(x[j][3])));
       }
       reduce_rows_over_half_wave<kValu>(p, c4, AddOp{});
       if ((c4 & 1) == 0) key_sum[8 * ((c4 >> 1) & 15) + group] = p[0];
@@ -646,7 +660,7 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
         double acc = 0.0;
 #pragma unroll
         for (int j = 0; j < kRowsPerThread; ++j) {
-          acc += static_cast<double>(fabsf(input(j, i)));
+          acc += static_cast<double>(fabsf(x[j][i]));
         }
         p[i] = with_partner<kValu, 32>(acc, AddOp{});
       }
@@ -715,18 +729,33 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
   // ---- m = r / s and the per-value scales max |m| over keys ----------------
   // The branch is uniform over the workgroup; each side is straight-line code.
   float mx[kRowsPerThread];
-  if constexpr (kPacked) {
-    if (fast_divide) {
-      max_of_quotients<kLayout, true, kValu>(raw, s_shared, s_inverse, group, c4, mx);
-    } else {
-      max_of_quotients<kLayout, false, kValu>(raw, s_shared, s_inverse, group, c4, mx);
+  if constexpr (kKeepProduct) {
+    if (!fast_divide) {
+      // Rare: the whole encode from the rows read again.  Returning here
+      // leaves x one path from phase 2 to the codes; a merge of the two paths
+      // would tie q0 to the registers of r and cost a copy per value.
+      reloaded_quotient_max<kValu>(tile, s_shared, group, c4, mx);
+      const bool fast_scale = finish_value_key_scales(mx, scale_shared, scale_inverse,
+                                                      code_factor, scales + item * kDim, t,
+                                                      group, c4);
+      write_codes_reloaded(tile, s_shared, scale_shared, scale_inverse, group, c4,
+                           codes + item * kTile, fast_scale);
+      return;
     }
+    products_and_max<kValu>(x, s_shared, s_inverse, c4, mx);
+    int8_t* out = codes + item * kTile;
+    if (finish_value_key_scales(mx, scale_shared, scale_inverse, code_factor,
+                                scales + item * kDim, t, group, c4)) {
+      write_codes_from_products(x, s_shared, s_inverse, scale_shared, scale_inverse,
+                                code_factor, group, c4, out);
+    } else {
+      write_codes_reloaded(tile, s_shared, scale_shared, scale_inverse, group, c4, out, false);
+    }
+    return;
+  } else if (fast_divide) {
+    smooth_and_max<kLayout, true, kValu>(x, s_shared, s_inverse, group, c4, mx);
   } else {
-    if (fast_divide) {
-      smooth_and_max<kLayout, true, kValu>(x, s_shared, s_inverse, group, c4, mx);
-    } else {
-      smooth_and_max<kLayout, false, kValu>(x, s_shared, s_inverse, group, c4, mx);
-    }
+    smooth_and_max<kLayout, false, kValu>(x, s_shared, s_inverse, group, c4, mx);
   }
   if constexpr (kLayout == kKeyValue) {
 #pragma unroll
@@ -759,18 +788,7 @@ __global__ __launch_bounds__(kThreads) void encode_kernel(
 
   // ---- codes ---------------------------------------------------------------
   int8_t* out = codes + item * kTile;
-  if constexpr (kPacked) {
-    if (fast_scale && fast_divide) {
-      write_codes_wide<kLayout>(raw, s_shared, s_inverse, scale_shared, scale_inverse,
-                                code_factor, group, c4, out);
-    } else if (fast_scale) {
-      write_codes_packed<kLayout, true>(raw, s_shared, scale_shared, scale_inverse, group, c4,
-                                        out);
-    } else {
-      write_codes_packed<kLayout, false>(raw, s_shared, scale_shared, scale_inverse, group, c4,
-                                         out);
-    }
-  } else if (fast_scale && fast_divide) {  // m finite: every r / s took the fast division
+  if (fast_scale && fast_divide) {  // m finite: every r / s took the fast division
     write_codes_lifted<kLayout>(x, scale_shared, scale_inverse, code_factor, group, c4, out);
   } else if (fast_scale) {
     write_codes<kLayout, true>(x, scale_shared, scale_inverse, group, c4, out);

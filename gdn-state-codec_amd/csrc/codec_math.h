@@ -89,23 +89,30 @@ constexpr float kCodeLiftMargin = 0x1p-13f;
 
 GDN_HD float code_lift(float m, float factor) { return fmaf(m, factor, kCodeLiftOffset); }
 
-// The same code formed from the stage's input r instead of m = RN(r / s), for
-// an encoder that does not keep m: u = RN(RN(r * y) * factor + 0.5 + 2^-13)
-// with y = RN(1 / s) and factor = RN(127 / scale).  Preconditions: m = RN(r / s)
+// The same code formed from the product q0 = RN(r * y) of the stage's input r
+// and y = RN(1 / s) (the first step of the reciprocal division of r by s), for
+// an encoder that keeps q0 instead of m = RN(r / s): u = RN(q0 * factor + 0.5 +
+// 2^-14) with factor = RN(127 / scale).  Preconditions: m = RN(r / s)
 // satisfies |m| <= scale, r * y and r / s are 0 or normal, factor as above.
 // With A = r / s, p = RN(RN(m / scale) * 127) = 127 A / scale (1+d0)(1+d1)(1+d2)
-// and Y = RN(r * y) * factor = 127 A / scale (1+e1)(1+e2)(1+e3), all |di|, |ei|
+// and Y = q0 * factor = 127 A / scale (1+e1)(1+e2)(1+e3), all |di|, |ei|
 // <= 2^-24, and |A / scale| <= 1 + 2^-24, so |p - Y| <= 127 * 6.01 * 2^-24 <
-// 2^-14.4; the lift's rounding adds at most 2^-18, so p + 0.5 lies within
-// 2^-14.3 of u - 2^-13.  If fract(u) >= 2^-12, p + 0.5 lies strictly between
-// floor(u) and floor(u) + 1 (2^-12 - 2^-13 > 2^-14.3 on the low side, 2^-13 >
-// 2^-14.3 on the high side): no tie, and lround(p) = floor(u).  Values with
-// fract(u) < 2^-12 (about 1 in 4,096) take the exact path.
-constexpr float kWideLiftOffset = 0.5f + 0x1p-13f;
-constexpr float kWideLiftMargin = 0x1p-12f;
+// 2^-14.42; the lift's rounding adds at most 2^-18, so p + 0.5 lies within
+// eps = 2^-14.3 of u - 2^-14.  If fract(u) >= 2^-13, p + 0.5 lies strictly
+// between floor(u) and floor(u) + 1 (2^-13 - 2^-14 > eps on the low side,
+// 2^-14 > eps on the high side): no tie, and lround(p) = floor(u).  Values
+// with fract(u) < 2^-13 (about 1 in 8,192) take the exact path.
+constexpr float kWideLiftOffset = 0.5f + 0x1p-14f;
+constexpr float kWideLiftMargin = 0x1p-13f;
 
-GDN_HD float wide_code_lift(float r, float reciprocal, float factor) {
-  return fmaf(r * reciprocal, factor, kWideLiftOffset);
+GDN_HD float wide_code_lift(float q0, float factor) {
+  return fmaf(q0, factor, kWideLiftOffset);
+}
+
+// The exact path's m = RN(r / s) from the kept product q0 = RN(r * y): the
+// remaining two steps of div_by_reciprocal(r, s, y).
+GDN_HD float quotient_from_product(float q0, float r, float s, float y) {
+  return fmaf(fmaf(-q0, s, r), y, q0);
 }
 
 // x - floor(x); on the device one v_fract_f32 (which returns the largest float
@@ -145,6 +152,15 @@ GDN_HD uint16_t float_to_bf16(float value) {
   v.f = value;
   const uint32_t lsb = (v.u >> 16) & 1u;
   return static_cast<uint16_t>((v.u + 0x7FFFu + lsb) >> 16);
+}
+
+// A bf16 input r recovered from q0 = RN(r * y), y = RN(1 / s): r is the bf16
+// nearest RN(q0 * s).  q0 * s = r (1+e1)(1+e2)(1+e3) with |ei| <= 2^-24, within
+// 2^-22.4 |r| of r, while the bf16 neighbours of r (8 significant bits) are at
+// least 2^-8 |r| away, so the nearest bf16 is r itself for every r whose
+// product and quotient are 0 or normal (the sign of a zero is kept).
+GDN_HD float bf16_input_from_product(float q0, float s) {
+  return bf16_to_float(float_to_bf16(q0 * s));
 }
 
 }  // namespace gdn

@@ -28,15 +28,19 @@
 //   codec_math_check lift_refit      the same sweep against the refit re-encode's
 //                                    rounding, trunc(RN(q +- 0.5)) clamped to +-127
 //                                    (window_boundary.cpp:336-345)
-//   codec_math_check wide_lift       the bf16 encoder's codes from its input r:
-//                                    wherever lift_fraction(wide_code_lift(r,
-//                                    RN(1/s), RN(127/scale))) >= kWideLiftMargin,
-//                                    its floor is clamp(lround(RN(RN(RN(r/s)/scale)
-//                                    *127)), -127, 127); 16,384 random (s, scale)
-//                                    pairs over the fast domains, scale the
-//                                    quotient of a random bf16 maximum, times every
-//                                    bf16 r with |RN(r/s)| <= scale.  The count of
-//                                    values left to the exact path goes to stderr.
+//   codec_math_check wide_lift       the bf16 encoder's codes from the product
+//                                    q0 = RN(r * RN(1/s)) of its input r: wherever
+//                                    lift_fraction(wide_code_lift(q0,
+//                                    RN(127/scale))) >= kWideLiftMargin, its floor
+//                                    is clamp(lround(RN(RN(RN(r/s)/scale)*127)),
+//                                    -127, 127); and r recovered from q0
+//                                    (bf16_input_from_product) bit for bit, and
+//                                    quotient_from_product(q0, r, ...) == RN(r/s);
+//                                    16,384 random (s, scale) pairs over the fast
+//                                    domains, scale the quotient of a random bf16
+//                                    maximum, times every bf16 r with |RN(r/s)| <=
+//                                    scale.  The count of values left to the exact
+//                                    path goes to stderr.
 //   codec_math_check order           xcd_contiguous_item (work_order.h) is a
 //                                    bijection on 0 .. n-1 for every n up to
 //                                    4096 and for the bench grids
@@ -283,7 +287,8 @@ void check_lift() {
 }
 
 // The bf16 encoder's direct lift (codec_math.h, wide_code_lift) against the
-// reference chain on every bf16 input of random (s, scale) pairs.  s is drawn
+// reference chain on every bf16 input of random (s, scale) pairs, with the
+// exact path's recovery of r and of m from the kept product.  s is drawn
 // over [2^-14, 2^20] (the smoothing's fast-division domain; s >= sqrt(1e-8)),
 // the scale is |RN(R / s)| for a random bf16 R chosen so that it lies in
 // [2^-90, 2^90], and r runs over every finite bf16 with |r| >= 2^-100 or
@@ -309,7 +314,11 @@ void check_wide_lift() {
       const float m = r / s;
       if (!(fabsf(m) <= scale)) continue;
       ++n;
-      const float u = gdn::wide_code_lift(r, y, factor);
+      const float q0 = r * y;
+      const float back = gdn::bf16_input_from_product(q0, s);
+      if (memcmp(&back, &r, sizeof(r)) != 0) ++bad;
+      if (!(gdn::quotient_from_product(q0, r, s, y) == m)) ++bad;
+      const float u = gdn::wide_code_lift(q0, factor);
       if (!(gdn::lift_fraction(u) >= gdn::kWideLiftMargin)) {
         ++fb;
         continue;

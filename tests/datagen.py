@@ -58,6 +58,24 @@ def tiny_head(seed: int) -> np.ndarray:
     return np.ascontiguousarray(x)
 
 
+def tiny_value_head(seed: int, value_axis: int) -> np.ndarray:
+    """Ordinary entries except two values (lines along `value_axis`: 0 for the
+    [value][key] layout, 1 for [key][value]) whose every entry has magnitude in
+    [2^-100, 2^-98): their scales max |r / s| fall below 2^-90 while every
+    non-zero |r| stays at or above 2^-100, so the encoder's fast division by s
+    applies and its fast division by the scale does not."""
+    g = rng(seed)
+    x = (g.standard_normal((DIM, DIM)) * 0.05).astype(np.float32)
+    for value in (11, 90):
+        line = np.ldexp(1.0 + g.random(DIM), g.integers(-100, -99, size=DIM, endpoint=True))
+        line = (line * np.where(g.random(DIM) < 0.5, -1.0, 1.0)).astype(np.float32)
+        if value_axis == 0:
+            x[value, :] = line
+        else:
+            x[:, value] = line
+    return np.ascontiguousarray(x)
+
+
 def huge_head(seed: int) -> np.ndarray:
     g = rng(seed)
     return np.ascontiguousarray((g.standard_normal((DIM, DIM)) * 1e30).astype(np.float32))

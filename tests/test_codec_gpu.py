@@ -153,7 +153,8 @@ def test_config1_round_trip_matches_reference_digests(device):
 
 
 @pytest.mark.parametrize("layout", [KV, VK])
-@pytest.mark.parametrize("kind", ["c1", "student_t", "wide", "tiny_and_huge", "requantize"])
+@pytest.mark.parametrize("kind", ["c1", "student_t", "wide", "tiny_and_huge", "tiny_value",
+                                  "requantize"])
 def test_encode_decode_match_oracle_on_random_heads(device, layout, kind):
     print(f"random parity layout={layout} kind={kind}", flush=True)
     if kind == "c1":
@@ -165,6 +166,9 @@ def test_encode_decode_match_oracle_on_random_heads(device, layout, kind):
     elif kind == "tiny_and_huge":
         x = np.stack([datagen.tiny_head(200 + i) for i in range(24)]
                      + [datagen.huge_head(300 + i) for i in range(24)])
+    elif kind == "tiny_value":
+        axis = 1 if layout == KV else 0
+        x = np.stack([datagen.tiny_value_head(350 + i, axis) for i in range(16)])
     else:
         # A window boundary re-encodes dequantized states: every code 0 became
         # an exact zero.  Half of those zeros are made -0.

@@ -63,14 +63,16 @@ def test_pool_encode_decode_match_oracle(device, bf16, layout):
 
 
 @pytest.mark.parametrize("layout", [KV, VK])
-@pytest.mark.parametrize("kind", ["c1", "student_t", "wide", "tiny_and_huge", "zeros",
-                                  "requantize"])
+@pytest.mark.parametrize("kind", ["c1", "student_t", "wide", "tiny_and_huge", "tiny_value",
+                                  "zeros", "requantize"])
 def test_bf16_pool_encode_edge_cases_match_oracle(device, layout, kind):
-    """bf16 tiles are encoded from their packed form: the codes on the fast
-    domains come from the input directly (the certified lift of codec_math.h),
-    with the exact path for values inside its margin, and the IEEE paths for
-    tiles outside the fast domains (subnormal and 1e30-scale entries).  Every
-    kind of tile the fp32 parity test uses, rounded to bf16, bit-exact."""
+    """bf16 tiles in [value][key] keep q0 = RN(r * RN(1/s)) on the fast
+    domains: the codes come from it directly (the certified lift of
+    codec_math.h), with the exact path, which recovers r from q0, for values
+    inside its margin; tiles outside the fast domains read their rows again
+    (subnormal and 1e30-scale entries: the division by s; values whose scale
+    is below 2^-90: the division by the scale).  Every kind of tile the fp32
+    parity test uses, rounded to bf16, bit-exact in both layouts."""
     print(f"bf16 pool edge cases layout={layout} kind={kind}", flush=True)
     if kind == "c1":
         x = datagen.c1_heads(64, 15)
@@ -81,6 +83,9 @@ def test_bf16_pool_encode_edge_cases_match_oracle(device, layout, kind):
     elif kind == "tiny_and_huge":
         x = np.stack([datagen.tiny_head(500 + i) for i in range(12)]
                      + [datagen.huge_head(600 + i) for i in range(12)])
+    elif kind == "tiny_value":
+        axis = 1 if layout == KV else 0
+        x = np.stack([datagen.tiny_value_head(650 + i, axis) for i in range(12)])
     elif kind == "zeros":
         x = np.stack([datagen.zero_rows_cols_head(700 + i) for i in range(16)])
     else:
