@@ -90,12 +90,14 @@ def test_lifted_codes_match_the_refit_rounding_wherever_the_margin_admits_them(c
 
 
 def test_bf16_direct_lift_matches_lround_wherever_its_margin_admits_it(checker):
-    """The bf16 pool encoder's codes formed from the input r without keeping
-    m = r / s (wide_code_lift in codec_math.h) against clamp(lround(RN(RN(RN(r/s)
-    / scale) * 127))) in IEEE fp32: every bf16 r of 16,384 random (s, scale)
-    pairs over the fast domains.  With the margin lowered to 2^-20, or the
-    offset to 0.5, this check fails (thousands of mismatches), so the margin
-    and the offset are what make it pass."""
+    """The bf16 pool encoder's codes formed from the kept product
+    q0 = RN(r * RN(1/s)) (wide_code_lift in codec_math.h) against
+    clamp(lround(RN(RN(RN(r/s) / scale) * 127))) in IEEE fp32, and the exact
+    path's recovery of r (bit for bit) and of m = RN(r/s) from q0: every bf16 r
+    of 16,384 random (s, scale) pairs over the fast domains.  With the margin
+    lowered to 2^-15 (34,537 mismatches), the offset to 0.5 (6,280), or the
+    recovery's rounding to bf16 left out (1.2e8), this check fails, so those
+    are what make it pass."""
     rc, checked, failures = _run(checker, "wide_lift")
     assert checked > 400_000_000 and failures == 0 and rc == 0
 
