@@ -2021,6 +2021,69 @@ def profile_pass(codec_only: bool = False) -> int:
     return 0
 
 
+def placement_pass(buffers: int = 4, rounds: int = 2) -> int:
+    """The config-2 dequantize into `buffers` separately allocated 16 GB output
+    buffers, from two 4 GB code buffers, with each output buffer's own plain
+    write and read probes (nontemporal, XCD-contiguous) and the 1:4 expand
+    probe on the same (codes, output) pair.  Placement in physical memory is
+    the driver's; the rates it gives a buffer are what this pass shows.  One
+    JSON line; every decode output is checked equal to the first."""
+    import torch
+
+    from gdn_state_codec import codec
+
+    lib = _probe_library()
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20261201)
+    state = torch.randn(C2_SHAPE, generator=gen, device=dev, dtype=torch.float32).mul_(0.05)
+    codes = [torch.empty(C2_SHAPE, dtype=torch.int8, device=dev) for _ in range(2)]
+    smoothing = torch.empty(C2_SHAPE[:-1], dtype=torch.float32, device=dev)
+    scales = torch.empty(C2_SHAPE[:-1], dtype=torch.float32, device=dev)
+    layout = codec.LAYOUT_KEY_VALUE
+    codec.encode(state, layout, codes[0], smoothing, scales)
+    codes[1].copy_(codes[0])
+    outs = [state] + [torch.empty_like(state) for _ in range(buffers - 1)]
+    sink = torch.empty(lib.gdn_hbm_probe_grid() * 256, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    tiles = state.numel() // (128 * 128)
+    nbytes = state.numel() * 4
+
+    def timed(fn, reps=5):
+        fn()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        for _ in range(reps):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]) / reps
+
+    reference = None
+    rows = []
+    for rnd in range(rounds):
+        for i, out in enumerate(outs):
+            row = {"round": rnd, "output": i,
+                   "write_GBps": nbytes / timed(lambda: lib.gdn_hbm_probe_write(
+                       stream, out.data_ptr(), nbytes, 3)) / 1e6,
+                   "read_GBps": nbytes / timed(lambda: lib.gdn_hbm_probe_read(
+                       stream, out.data_ptr(), sink.data_ptr(), nbytes, 3)) / 1e6}
+            for c, code in enumerate(codes):
+                row[f"codes{c}_decode_ms"] = timed(
+                    lambda: codec.decode(code, smoothing, scales, layout, out=out))
+                if reference is None:
+                    reference = out.clone()
+                elif not torch.equal(out, reference):
+                    raise RuntimeError("dequantize outputs differ between buffers")
+                row[f"codes{c}_expand_ms"] = timed(lambda: lib.gdn_hbm_probe_expand(
+                    stream, code.data_ptr(), out.data_ptr(), tiles, 3))
+            _log(json.dumps(row))
+            rows.append(row)
+    print(json.dumps({"placement_pass": "config 2 dequantize", "buffers": buffers,
+                      "rounds": rounds, "rows": rows}), flush=True)
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -2034,6 +2097,8 @@ def main() -> int:
                         help="a few launches of every kernel, for rocprofv3 counter passes")
     parser.add_argument("--profile-codec", action="store_true",
                         help="the --profile launches of the config-2 codec and the probes only")
+    parser.add_argument("--placement", action="store_true",
+                        help="the config-2 dequantize and HBM probes on several output buffers")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every head "
@@ -2049,6 +2114,8 @@ def main() -> int:
     torch.cuda.init()
     if args.profile or args.profile_codec:
         return profile_pass(codec_only=args.profile_codec)
+    if args.placement:
+        return placement_pass()
     box = {"before": _box_info()}
     state, codes, smoothing, scales, dense, enc_ms, dec_ms, wall_ms = bench_codec(
         args.steps, args.warmup)
