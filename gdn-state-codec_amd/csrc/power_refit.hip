@@ -27,6 +27,7 @@
 #include <mutex>
 #include <type_traits>
 
+#include "pipelined_sum.h"
 #include "codec_math.h"
 #include "gdn_state_codec_window.h"
 #include "lane_exchange.h"
@@ -119,12 +120,25 @@ __device__ __forceinline__ float code_value(const PowerShared& sh, int8_t code) 
   return sh.code_value[static_cast<uint8_t>(code)];
 }
 
+// The same value by arithmetic, div_by_127 of the code (the two-part division,
+// exact for every integer in [-128, 127]): in the operator's sums it replaces
+// a second LDS read, whose address depends on the first, with two VALU
+// instructions.
+__device__ __forceinline__ float code_value_arith(int8_t code) {
+  return div_by_127(static_cast<float>(code));
+}
+
 // Normalize (:25-37) of v; returns whether the norm was usable.  The squared
 // norm is one sequential sum on thread 0.
 __device__ bool normalize(PowerShared& sh, float* v, int t) {
   if (t == 0) {
     float squared = 0.0f;
-    for (int i = 0; i < kDim; ++i) squared += v[i] * v[i];
+    struct Group {
+      float x[16];
+    };
+    pipelined<kDim / 16, Group>(
+        [&](auto g, Group& r) { unrolled<16>([&](auto i) { r.x[i] = v[16 * decltype(g)::value + i]; }); },
+        [&](auto, const Group& r) { unrolled<16>([&](auto i) { squared += r.x[i] * r.x[i]; }); });
     sh.flag = squared <= 1.0e-20f ? 0 : 1;
     sh.scalar = sh.flag ? 1.0f / newton_sqrt(squared) : 0.0f;
   }
@@ -173,7 +187,7 @@ __device__ void apply_right(PowerShared& sh, const float* vector, float* output,
   float value = 0.0f;
   const float s = sh.smoothing[row];
   for (int column = 0; column < kDim; ++column) {
-    value += code_value(sh, sh.code[column * kCodeStride + row]) * s * sh.scales[column] *
+    value += code_value_arith(sh.code[column * kCodeStride + row]) * s * sh.scales[column] *
              vector[column] * bs;
   }
   for (int r = 0; r < kRank; ++r) value += h2f(sh.ck[row * kRank + r]) * sh.old_projection[r] * bs;
@@ -195,7 +209,7 @@ __device__ void apply_transpose(PowerShared& sh, const float* vector, float* out
   const float scale = sh.scales[column];
   const int8_t* code = sh.code + column * kCodeStride;
   for (int row = 0; row < kDim; ++row) {
-    value += code_value(sh, code[row]) * sh.smoothing[row] * scale * vector[row] * bs;
+    value += code_value_arith(code[row]) * sh.smoothing[row] * scale * vector[row] * bs;
   }
   for (int r = 0; r < kRank; ++r) value += h2f(sh.cv[column * kRank + r]) * sh.old_projection[r] * bs;
   for (int j = 0; j < kWindow; ++j) {
