@@ -305,13 +305,52 @@ def test_int8_matmul_and_int8_vector_are_exact(device, transpose_a):
     axis = (0.5 + g.random((states, 128))).astype(np.float32)
     q = torch.full((states, 128, 16), 7, dtype=torch.int8, device=device)
     dyn = torch.zeros((states, 8), dtype=torch.float32, device=device)
+    dx, daxis = dev(x, device), dev(axis, device)  # held: a freed temporary's block is reused
     assert native().prepare_int8_vector_launch_v1(
-        stream(), dev(x, device).data_ptr(), dev(axis, device).data_ptr(), q.data_ptr(),
-        dyn.data_ptr(), states) == 0
+        stream(), dx.data_ptr(), daxis.data_ptr(), q.data_ptr(), dyn.data_ptr(), states) == 0
     q_ref, dyn_ref = W.prepare_int8_vector(x, axis)
     torch.cuda.synchronize()
     assert np.array_equal(q.cpu().numpy(), q_ref)
     assert dyn.cpu().numpy()[:, 0].tobytes() == dyn_ref[:, 0].tobytes()
+
+
+def test_int8_split_edges_round_by_the_float_half_add(device):
+    """The hi/lo split and the int8 vector on inputs at the reference's rounding
+    edges (.5 ties, 0.5 - 2^-25): codes derived by hand, and the oracle's."""
+    x, s, hi, lo, lo_scale = WG.split_tie_state()
+    states = 3
+    print("int8 split rounding edges", flush=True)
+    reads = np.tile(x.astype(np.float16).view(np.uint16), (states, 1))
+    axis = np.tile(s, (states, 1))
+    quantized = torch.full((states, 128, 16), 7, dtype=torch.int8, device=device)
+    dyn = torch.zeros((states, 8), dtype=torch.float32, device=device)
+    dr, ddecay = dev(reads, device), dev(np.ones(states, np.float32), device)
+    daxis = dev(axis, device)
+    assert native().prepare_decode_pair_launch_v1(
+        stream(), dr.data_ptr(), dr.data_ptr(), ddecay.data_ptr(), daxis.data_ptr(),
+        quantized.data_ptr(), dyn.data_ptr(), states) == 0
+    q_ref, dyn_ref = W.prepare_decode_pair(reads, reads, np.ones(states, np.float32), axis)
+    torch.cuda.synchronize()
+    q, d = quantized.cpu().numpy(), dyn.cpu().numpy()
+    assert np.array_equal(q, q_ref)
+    assert d[:, :4].tobytes() == dyn_ref[:, :4].tobytes()
+    for c in range(2):
+        assert (q[:, :, 2 * c] == hi).all() and (q[:, :, 2 * c + 1] == lo).all()
+        assert (d[:, c] == np.float32(0.125)).all() and (d[:, 2 + c] == lo_scale).all()
+    operand = np.zeros((states, 128, 16), np.float16)
+    operand[:, :, 0] = x.astype(np.float16)
+    vq = torch.full((states, 128, 16), 7, dtype=torch.int8, device=device)
+    vdyn = torch.zeros((states, 8), dtype=torch.float32, device=device)
+    doperand = dev(operand.view(np.uint16), device)
+    assert native().prepare_int8_vector_launch_v1(
+        stream(), doperand.data_ptr(), daxis.data_ptr(), vq.data_ptr(), vdyn.data_ptr(),
+        states) == 0
+    vq_ref, vdyn_ref = W.prepare_int8_vector(operand.view(np.uint16), axis)
+    torch.cuda.synchronize()
+    got = vq.cpu().numpy()
+    assert np.array_equal(got, vq_ref) and (got[:, :, 0] == hi).all()
+    assert vdyn.cpu().numpy()[:, 0].tobytes() == vdyn_ref[:, 0].tobytes()
+    assert (vdyn.cpu().numpy()[:, 0] == np.float32(0.125)).all()
 
 
 @pytest.mark.parametrize("states", [64, 1024])

@@ -221,3 +221,38 @@ def test_decode_pair_chain_matches_windowed_step_within_vector_quantization():
     live = buf["positions"][:, 0] < 16
     tol = bound + 0.5 * ulp(out64 + bound, 7)
     assert (np.abs(got - out64)[live] <= tol[live]).all()
+
+
+def test_int8_split_rounds_by_the_float_half_add():
+    """The oracle's hi/lo split (prepare_decode_pair) against codes derived by
+    hand from the reference's rounding on inputs at its edges: .5 ties round
+    away from zero, and 0.5 - 2^-25 rounds up because the float add itself
+    rounds.  Round-half-even (np.rint) and exact round-half-away (lround) both
+    give different codes on these rows, so either slip fails this test."""
+    x, s, hi, lo, lo_scale = WG.split_tie_state()
+    f16 = x.astype(np.float16)
+    assert np.array_equal(f16.astype(np.float32), x)  # every input is exact in fp16
+    reads = f16.view(np.uint16)[None]
+    q, dyn = W.prepare_decode_pair(reads, reads, np.ones(1, np.float32), s[None])
+    for c in range(2):  # both vectors of the pair: the read and the output side
+        assert np.array_equal(q[0, :, 2 * c], hi)
+        assert np.array_equal(q[0, :, 2 * c + 1], lo)
+        assert dyn[0, c] == np.float32(0.125)
+        assert dyn[0, 2 + c] == lo_scale
+    assert not q[0, :, 4:].any()
+    exact = (x.astype(np.float64) * s) / 0.125
+    assert not np.array_equal(np.rint(exact).astype(np.int8), hi)        # ties-to-even
+    assert not np.array_equal((np.sign(exact) * np.floor(np.abs(exact) + 0.5)).clip(-127, 127)
+                              .astype(np.int8), hi)                      # exact half-away
+
+
+def test_int8_vector_rounds_by_the_float_half_add():
+    """prepare_int8_vector (encoded_projection.cpp:179-234) on the same edge
+    inputs, column 0 of an fp16 [128][16] operand: one level, the hi codes."""
+    x, s, hi, _, _ = WG.split_tie_state()
+    operand = np.zeros((1, 128, 16), np.float16)
+    operand[0, :, 0] = x.astype(np.float16)
+    q, dyn = W.prepare_int8_vector(operand.view(np.uint16), s[None])
+    assert np.array_equal(q[0, :, 0], hi)
+    assert not q[0, :, 1:].any()
+    assert dyn[0, 0] == np.float32(0.125)

@@ -122,3 +122,30 @@ def capsule_at(buf: dict, state: int, layout: int, rank: int = 4) -> W.CapsuleWi
     import ctypes
     cap.position = ctypes.c_uint32(int(buf["positions"][state, 0]))
     return cap
+
+
+def split_tie_state():
+    """One state whose hi-level divisions land on the reference's rounding
+    edges (encoded_projection.cpp:289-296, :326-334: add +-0.5 in float, clamp
+    to +-127, truncate).  The largest |x * s| is 15.875 = 127 / 8, so the hi
+    scale is exactly 1/8 and x * s / scale is exact:
+      row 1:  0.3125            ->  2.5          -> 3   (ties-to-even: 2)
+      row 2: -0.3125            -> -2.5          -> -3  (ties-to-even: -2)
+      row 3:  2^-4 * (1-2^-24)  ->  0.5 - 2^-25  -> 1   (exact rounding: 0;
+              the float add 0.5 - 2^-25 + 0.5 ties to even at 1.0)
+      row 4:  1.0               ->  8.0          -> 8
+      row 0: 15.875             ->  127          -> 127 (127.5 clamps)
+    and every other row is 0 (0 + 0.5 truncates to 0)."""
+    x = np.zeros(128, np.float32)
+    x[:5] = [15.875, 0.3125, -0.3125, 2.0 ** -4, 1.0]
+    s = np.ones(128, np.float32)
+    s[3] = np.float32(1.0) - np.float32(2.0 ** -24)
+    hi = np.zeros(128, np.int8)
+    hi[:5] = [127, 3, -3, 1, 8]
+    # The residuals x*s - hi/8 are 0 except rows 1-3; their largest magnitude
+    # is 2^-4 + 2^-28 (row 3), which sets the lo scale; rows 1 and 3 map to
+    # -127 and row 2 to 127 (126.9999995 +- 0.5, clamped).
+    lo = np.zeros(128, np.int8)
+    lo[1:4] = [-127, 127, -127]
+    lo_scale = np.float32(np.float32(2.0 ** -4 + 2.0 ** -28) / np.float32(127.0))
+    return x, s, hi, lo, lo_scale
