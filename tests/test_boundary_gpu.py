@@ -130,6 +130,36 @@ def test_power_refit_is_bit_exact(device, iterations):
     assert dw.cpu().numpy().tobytes() == ref_ws.tobytes()
 
 
+@pytest.mark.parametrize("iterations", [1, 32])
+def test_power_refit_of_a_rank_one_window_in_closed_form(device, iterations):
+    """Windows whose operator is exactly rank one: the kernel's compensators,
+    workspace and codes follow the closed form (the fitted pair at the first
+    rank whose start vector touches the column, the other ranks' start vectors
+    stored as values), and every output equals the oracle's."""
+    from test_boundary_oracle import RANK_ONE_COLUMNS, check_rank_one_fit, rank_one_window
+
+    columns = RANK_ONE_COLUMNS
+    states = len(columns)
+    print(f"power refit, rank-one windows, iterations={iterations}", flush=True)
+    buf, k = rank_one_window(columns, 311 + iterations)
+    out = sentinel_outputs(states)
+    workspace = np.full((states, 128, 128), 7.0, np.float32)
+    d, do = to_device(buf, device), to_device(out, device)
+    dw = dev(workspace, device)
+    assert native().window_boundary_launch_v1(
+        stream(), *window_ptrs(d), *out_ptrs(do), dw.data_ptr(), states, iterations) == 0
+    torch.cuda.synchronize()
+    got, ws = from_device(do, out), dw.cpu().numpy()
+    for s, j in enumerate(columns):
+        check_rank_one_fit(got["next_compensator_keys"][s], got["next_compensator_values"][s],
+                           ws[s], got["next_residual"][s], got["next_scales"][s], j, k[s])
+    ref, ref_out, ref_ws = WG.copy_buffers(buf), WG.copy_buffers(out), workspace.copy()
+    W.window_boundary_power(ref, ref_out, ref_ws, iterations)
+    assert_same(got, ref_out, OUT_NAMES)
+    assert_same(from_device(d, buf), ref, buf.keys())
+    assert ws.tobytes() == ref_ws.tobytes()
+
+
 def test_power_refit_with_tiny_rows_is_bit_exact(device):
     """States whose fitted residual has tiny rows (smoothing scaled by
     2^-110, records and compensators zero: non-zero cells below 2^-100 and

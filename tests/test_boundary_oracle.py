@@ -10,7 +10,10 @@ numpy float64:
 * the rank-4 power iteration finds a planted dominant singular pair and lowers
   the residual norm (the reference probe's acceptance criterion,
   window_boundary_runtime_probe.cpp:327-329);
-* the Newton square root is within 2 ulp of sqrt.
+* the Newton square root is within 2 ulp of sqrt;
+* on a window whose operator is exactly rank one (one record, one column) the
+  refit has a closed form that exposes the start vectors and the Newton root
+  of zero (check_rank_one_fit).
 """
 
 from __future__ import annotations
@@ -289,3 +292,107 @@ def test_newton_square_root_transcription():
     want = np.array([P.square_root(v) for v in values], np.float32)
     sqrt_c = W._bind_boundary(W._l()).gdn_oracle_boundary_sqrt
     assert np.array_equal(np.array([sqrt_c(float(v)) for v in values], np.float32), want)
+
+
+# The reference's start vectors, ((rank + 1) * (column + 3)) % 17 - 8
+# (window_boundary.cpp:268-271), one row per rank.
+START = (((np.arange(4)[:, None] + 1) * (np.arange(128)[None, :] + 3)) % 17 - 8).astype(np.float64)
+# s_0 at these columns: -5, -4, -3, 0, 4, 8, 0, 8, 3; where it is 0 the pair is
+# fitted at rank 1 (s_1 = 8 there).
+RANK_ONE_COLUMNS = (0, 1, 2, 5, 9, 13, 22, 64, 127)
+
+
+def rank_one_window(columns, seed):
+    """Full windows whose only content is the last record: key k (integers
+    +-1..6) times correction a e_j with a = 1/4, one column j per state; codes,
+    compensators and the other records zero, every gate 1 (the last record's
+    suffix is 1 whatever the gates).  The residual operator is exactly
+    k a e_j^T, and every product the refit forms from it is exact or rounds
+    the same way on both sides of a deflation."""
+    states = len(columns)
+    buf = WG.window_buffers(states, seed, VK, positions=16, compensated=False)
+    buf["residual"][:] = 0
+    buf["smoothing"][:] = 1.0
+    buf["scales"][:] = 1.0
+    buf["record_decay"][:] = 1.0
+    g = np.random.default_rng(seed)
+    k = (g.integers(1, 7, (states, 128)) * g.choice([-1, 1], (states, 128))).astype(np.float32)
+    keys = np.zeros((states, 16, 128), np.float32)
+    corr = np.zeros((states, 16, 128), np.float32)
+    keys[:, 15] = k
+    corr[np.arange(states), 15, list(columns)] = 0.25
+    buf["record_keys"] = keys.astype(np.float16).view(np.uint16)
+    buf["record_corrections"] = corr.astype(np.float16).view(np.uint16)
+    return buf, k
+
+
+def check_rank_one_fit(nk_bits, nv_bits, workspace, codes, scales, j, k):
+    """The refit of rank_one_window's state, in closed form.  Rank r starts
+    from s_r / |s_r|.  If s_r[j] != 0 (the first such rank, r*), one power step
+    maps it to sign(s_r[j]) e_j exactly after fp16 storage, and the stored pair
+    is (sign a k, sign e_j); the deflated operator is then exactly zero.  Every
+    other rank sees a zero operator: the first Normalize fails, the loop breaks,
+    and the final left vector is zero, whose 20-step Newton root is 2^-20 (from
+    1, halved 20 times), above the 1e-20 cut-off, so the rank stores zero keys
+    and fp16(s_r / |s_r|) as values.  A correctly rounded square root (0) would
+    store nothing; a misread start vector changes the stored values."""
+    nk = W.f16_to_f32(nk_bits).astype(np.float64)
+    nv = W.f16_to_f32(nv_bits).astype(np.float64)
+    fit = next(r for r in range(4) if START[r, j] != 0)
+    sign = np.sign(START[fit, j])
+    unit = np.zeros(128)
+    unit[j] = sign
+    assert np.array_equal(nk[:, fit], sign * 0.25 * k), (j, fit)
+    assert np.array_equal(nv[:, fit], unit), (j, fit)
+    for r in range(4):
+        if r == fit:
+            continue
+        exact = START[r] / np.linalg.norm(START[r])
+        assert not nk[:, r].any(), (j, r)
+        assert np.array_equal(nv[:, r], exact.astype(np.float16).astype(np.float64)), (j, r)
+    assert not np.asarray(workspace).any() and not np.asarray(codes).any()
+    assert not np.asarray(scales).any()
+
+
+def test_start_vector_margins_for_the_closed_form():
+    """check_rank_one_fit compares fp16(s_r / |s_r|) exactly: the float32
+    normalization is within a few units of 2^-24 of the exact quotient, so
+    every value must lie farther than 2^-18 (relative) from an fp16 rounding
+    midpoint, and does."""
+    for r in range(4):
+        exact = START[r] / np.linalg.norm(START[r])
+        nz = exact[exact != 0]
+        e = np.floor(np.log2(np.abs(nz)))
+        frac = np.abs(nz) / 2.0 ** (e - 10)          # units of the fp16 ulp
+        assert (np.abs(frac - np.floor(frac) - 0.5) > 2.0 ** -8).all(), r
+
+
+@pytest.mark.parametrize("iterations", [1, 4, 32])
+def test_power_refit_of_a_rank_one_window_in_closed_form(iterations):
+    """The oracle's power refit on rank_one_window against check_rank_one_fit;
+    the numpy transcription with a start vector shifted by one column or a
+    correctly rounded square root fails the same check."""
+    import powerfit_numpy as P
+
+    columns = RANK_ONE_COLUMNS
+    buf, k = rank_one_window(columns, 211 + iterations)
+    out = W.boundary_outputs(len(columns))
+    workspace = np.full((len(columns), 128, 128), 7.0, np.float32)
+    ref = WG.copy_buffers(buf)
+    W.window_boundary_power(ref, out, workspace, iterations)
+    for s, j in enumerate(columns):
+        check_rank_one_fit(out["next_compensator_keys"][s], out["next_compensator_values"][s],
+                           workspace[s], out["next_residual"][s], out["next_scales"][s], j, k[s])
+        assert (out["next_smoothing"][s] == out["next_smoothing"][s][0]).all()
+        assert abs(out["next_smoothing"][s][0] - 1e-4) < 2e-11
+        assert ref["positions"][s, 0] == 0 and not ref["record_keys"][s].any()
+    if iterations == 1:
+        s, j = 0, columns[0]
+        shifted = P.power_refit(buf, s, 1, start=lambda r: (
+            (((r + 1) * (np.arange(128) + 4)) % 17) - 8).astype(np.float32))
+        rounded = P.power_refit(buf, s, 1, sqrt=lambda v: np.float32(np.sqrt(v)))
+        for bad in (shifted, rounded):
+            with pytest.raises(AssertionError):
+                check_rank_one_fit(bad["next_compensator_keys"], bad["next_compensator_values"],
+                                   bad["workspace"], bad["next_residual"], bad["next_scales"],
+                                   j, k[s])
