@@ -76,8 +76,10 @@ struct PowerArgs {
 // read: 32,424 bytes, five workgroups per CU.
 struct PowerShared {
   int8_t code[kDim * kCodeStride];  // [value column][key row]
-  uint16_t ck[kDim * kRank], cv[kDim * kRank];
-  uint16_t nk[kDim * kRank], nv[kDim * kRank];
+  alignas(8) uint16_t ck[kDim * kRank];
+  alignas(8) uint16_t cv[kDim * kRank];
+  alignas(8) uint16_t nk[kDim * kRank];
+  alignas(8) uint16_t nv[kDim * kRank];
   // Records as [dimension][record]: a dimension's 16 records are 32
   // contiguous bytes, so the record projections (lane j walks record j)
   // read consecutive words and a cell reads its 16 records as two 16-byte
@@ -258,28 +260,35 @@ __device__ __forceinline__ void reencode_rows(PowerShared& sh, float bs, int t, 
     for (int j = 0; j < kWindow; ++j) {
       suffix[j] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sh.record_suffix[j])));
     }
-    const auto low = [](uint32_t pair, int i) { return h2f(i & 1 ? pair >> 16 : pair & 0xFFFFu); };
+    // Every compensator and record product is of two fp16 values, exact in
+    // fp32: one v_fma_mix_f32 each (half_product), and the fitted ranks'
+    // `value -= nk * nv` one fma (minus_half_product), the reference's
+    // roundings throughout.
+    const float neg_zero = opaque_negative_zero();
+    const auto half = [](uint32_t pair, int i) { return i & 1 ? pair >> 16 : pair; };
     each_column([&](auto c) {
       constexpr int column = decltype(c)::value;
-      // Opaque to the compiler, so the pairs are widened per column instead of
-      // once into 24 long-lived registers.
+      // Opaque to the compiler, so the pairs stay packed in registers.
 #pragma unroll
       for (int i = 0; i < kRank / 2; ++i) asm volatile("" : "+v"(ck2[i]), "+v"(nk2[i]));
 #pragma unroll
       for (int i = 0; i < kWindow / 2; ++i) asm volatile("" : "+v"(rk2[i]));
       float value = code_value(sh, sh.code[column * kCodeStride + row]) * s *
                     sh.scales[column] * bs;
+      const uint2 cv2 = *reinterpret_cast<const uint2*>(sh.cv + column * kRank);
+      const uint2 nv2 = *reinterpret_cast<const uint2*>(sh.nv + column * kRank);
+      const uint32_t cvp[kRank / 2] = {cv2.x, cv2.y}, nvp[kRank / 2] = {nv2.x, nv2.y};
 #pragma unroll
       for (int r = 0; r < kRank; ++r) {
-        value += low(ck2[r / 2], r) * h2f(sh.cv[column * kRank + r]) * bs;
-        value -= low(nk2[r / 2], r) * h2f(sh.nv[column * kRank + r]);
+        value += half_product(half(ck2[r / 2], r), half(cvp[r / 2], r), neg_zero) * bs;
+        value = minus_half_product(value, half(nk2[r / 2], r), half(nvp[r / 2], r));
       }
       const uint4* const rc4 = reinterpret_cast<const uint4*>(sh.rc + column * kWindow);
       const uint4 c0 = rc4[0], c1 = rc4[1];
       const uint32_t rc2[kWindow / 2] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
       for (int j = 0; j < kWindow; ++j) {
-        value += low(rk2[j / 2], j) * low(rc2[j / 2], j) * suffix[j];
+        value += half_product(half(rk2[j / 2], j), half(rc2[j / 2], j), neg_zero) * suffix[j];
       }
       cell[column] = value;
       // One column's operands at a time: the scheduler would otherwise hoist

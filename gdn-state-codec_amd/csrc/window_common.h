@@ -30,6 +30,33 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 }
 
+// -0.0f as a value the compiler cannot see through (one SGPR); see
+// half_product.
+__device__ __forceinline__ float opaque_negative_zero() {
+  uint32_t bits = 0x80000000u;
+  asm("" : "+s"(bits));
+  return __uint_as_float(bits);
+}
+
+// The product of two fp16 values (the low 16 bits of a_bits and b_bits) in
+// fp32. Their 11-bit significands multiply to at most 22 bits and the
+// exponents stay in the fp32 normal range, so the product is exact and equals
+// widening both operands and multiplying with one rounding. fma(a, b, -0)
+// computes it as one v_fma_mix_f32, which widens the halves (op_sel picks the
+// high half of a pair) inside the instruction; adding -0 leaves every product,
+// a signed zero included, unchanged. neg_zero must come from
+// opaque_negative_zero(): with a literal -0 the compiler turns the fma into a
+// multiply of two separately widened operands.
+__device__ __forceinline__ float half_product(uint32_t a_bits, uint32_t b_bits, float neg_zero) {
+  return __builtin_fmaf(half_bits_to_float(a_bits), half_bits_to_float(b_bits), neg_zero);
+}
+
+// value - a*b for fp16 a and b: the product is exact (half_product), so one
+// fma rounds exactly what the subtraction of the rounded product rounds.
+__device__ __forceinline__ float minus_half_product(float value, uint32_t a_bits, uint32_t b_bits) {
+  return __builtin_fmaf(-half_bits_to_float(a_bits), half_bits_to_float(b_bits), value);
+}
+
 // Round an fp32 value to nearest even fp16 (v_cvt_f16_f32), with fp16
 // subnormals. The empty asm pins `value` as a rounded fp32 register:
 // without it the compiler folds a producing multiply into v_fma_mixlo_f16,
