@@ -266,6 +266,26 @@ __device__ __forceinline__ void reencode_rows(PowerShared& sh, float bs, int t, 
     // roundings throughout.
     const float neg_zero = opaque_negative_zero();
     const auto half = [](uint32_t pair, int i) { return i & 1 ? pair >> 16 : pair; };
+    // A column's LDS operands; the next column's are read while this one's
+    // cell is evaluated, so their latency overlaps the arithmetic.
+    struct Operands {
+      int code;
+      float scale;
+      uint2 cv, nv;
+      uint4 r0, r1;
+    };
+    const auto fetch = [&](int column) {
+      Operands o;
+      o.code = sh.code[column * kCodeStride + row];
+      o.scale = sh.scales[column];
+      o.cv = *reinterpret_cast<const uint2*>(sh.cv + column * kRank);
+      o.nv = *reinterpret_cast<const uint2*>(sh.nv + column * kRank);
+      const uint4* const rc4 = reinterpret_cast<const uint4*>(sh.rc + column * kWindow);
+      o.r0 = rc4[0];
+      o.r1 = rc4[1];
+      return o;
+    };
+    Operands next = fetch(0);
     each_column([&](auto c) {
       constexpr int column = decltype(c)::value;
       // Opaque to the compiler, so the pairs stay packed in registers.
@@ -273,26 +293,27 @@ __device__ __forceinline__ void reencode_rows(PowerShared& sh, float bs, int t, 
       for (int i = 0; i < kRank / 2; ++i) asm volatile("" : "+v"(ck2[i]), "+v"(nk2[i]));
 #pragma unroll
       for (int i = 0; i < kWindow / 2; ++i) asm volatile("" : "+v"(rk2[i]));
-      float value = code_value(sh, sh.code[column * kCodeStride + row]) * s *
-                    sh.scales[column] * bs;
-      const uint2 cv2 = *reinterpret_cast<const uint2*>(sh.cv + column * kRank);
-      const uint2 nv2 = *reinterpret_cast<const uint2*>(sh.nv + column * kRank);
-      const uint32_t cvp[kRank / 2] = {cv2.x, cv2.y}, nvp[kRank / 2] = {nv2.x, nv2.y};
+      const Operands o = next;
+      if constexpr (column + 1 < kDim) next = fetch(column + 1);
+      // Issued here, ahead of this column's arithmetic, not sunk to its end.
+      __builtin_amdgcn_sched_barrier(0);
+      // code / 127 by the two-part division (exact for every integer code).
+      float value = code_value_arith(static_cast<int8_t>(o.code)) * s * o.scale * bs;
+      const uint32_t cvp[kRank / 2] = {o.cv.x, o.cv.y}, nvp[kRank / 2] = {o.nv.x, o.nv.y};
 #pragma unroll
       for (int r = 0; r < kRank; ++r) {
         value += half_product(half(ck2[r / 2], r), half(cvp[r / 2], r), neg_zero) * bs;
         value = minus_half_product(value, half(nk2[r / 2], r), half(nvp[r / 2], r));
       }
-      const uint4* const rc4 = reinterpret_cast<const uint4*>(sh.rc + column * kWindow);
-      const uint4 c0 = rc4[0], c1 = rc4[1];
-      const uint32_t rc2[kWindow / 2] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      const uint32_t rc2[kWindow / 2] = {o.r0.x, o.r0.y, o.r0.z, o.r0.w,
+                                         o.r1.x, o.r1.y, o.r1.z, o.r1.w};
 #pragma unroll
       for (int j = 0; j < kWindow; ++j) {
         value += half_product(half(rk2[j / 2], j), half(rc2[j / 2], j), neg_zero) * suffix[j];
       }
       cell[column] = value;
-      // One column's operands at a time: the scheduler would otherwise hoist
-      // the LDS reads of many columns ahead of their use.
+      // One column ahead at a time: the scheduler would otherwise hoist the
+      // LDS reads of many columns ahead of their use.
       __builtin_amdgcn_sched_barrier(0);
     });
   }
