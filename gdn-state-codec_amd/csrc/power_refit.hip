@@ -537,9 +537,11 @@ struct RequantizeArgs {
 // operator minus the committed ranks re-encoded.  The state is staged in the
 // power refit's LDS layout (codes transposed to [column][row], the [rank][dim]
 // bases to [dim][rank], the records to [dim][record]) and re-encoded by the
-// same reencode_rows; thread t packs the codes of its row in registers and
-// stores the row as eight 16-byte words.
-__global__ __launch_bounds__(kThreads) void encoded_requantize_kernel(RequantizeArgs a) {
+// same reencode_rows; the codes go back through the code area to 16-byte
+// row stores (168 VGPRs, three wavefronts per SIMD: five workgroups per CU,
+// as the LDS allows).
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void encoded_requantize_kernel(
+    RequantizeArgs a) {
   extern __shared__ __align__(16) unsigned char dynamic[];
   PowerShared& sh = *reinterpret_cast<PowerShared*>(dynamic);
   const int t = threadIdx.x;
@@ -581,19 +583,30 @@ __global__ __launch_bounds__(kThreads) void encoded_requantize_kernel(Requantize
   bs = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bs)));
   __syncthreads();
 
-  uint32_t packed[kDim / 4];
-#pragma unroll
-  for (int q = 0; q < kDim / 4; ++q) packed[q] = 0u;
+  // The codes of row t, four to a word, staged row-major in the code area
+  // (free once every cell has been evaluated; a 132-byte row stride keeps the
+  // 64 lanes' word writes in distinct banks), so that only one packed word is
+  // live at a time.
+  uint32_t quad = 0u;
   reencode_rows(sh, bs, t, a.workspace + state * kTile, a.next_smoothing + vb, a.next_scales + vb,
                 [&](auto c, int8_t code) {
                   constexpr int column = decltype(c)::value;
-                  packed[column / 4] |= static_cast<uint32_t>(static_cast<uint8_t>(code))
-                                        << (8 * (column % 4));
+                  quad |= static_cast<uint32_t>(static_cast<uint8_t>(code)) << (8 * (column % 4));
+                  if constexpr (column % 4 == 3) {
+                    *reinterpret_cast<uint32_t*>(&sh.code[t * kCodeStride + column - 3]) = quad;
+                    quad = 0u;
+                  }
                 });
-  uint4* const out = reinterpret_cast<uint4*>(a.next_residual + state * kTile + t * kDim);
+  __syncthreads();
+  // next_residual [row][column]: each round of 16 rows, eight lanes write one
+  // whole 128-byte row.
 #pragma unroll
-  for (int q = 0; q < kDim / 16; ++q) {
-    out[q] = make_uint4(packed[4 * q], packed[4 * q + 1], packed[4 * q + 2], packed[4 * q + 3]);
+  for (int round = 0; round < kDim / 16; ++round) {
+    const int row = 16 * round + (t >> 3);
+    const int offset = 16 * (t & 7);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&sh.code[row * kCodeStride + offset]);
+    *reinterpret_cast<uint4*>(a.next_residual + state * kTile + row * kDim + offset) =
+        make_uint4(src[0], src[1], src[2], src[3]);
   }
   // The committed bases in the [dim][rank] layout: the LDS copies already are.
   for (int i = t; i < kDim * kRank; i += kThreads) {
