@@ -2021,6 +2021,74 @@ def profile_pass(codec_only: bool = False) -> int:
     return 0
 
 
+def lds_residency_pass(wait_ticks: int = 20000, repeats: int = 3) -> int:
+    """How many workgroups share a CU as a function of their LDS size
+    (csrc/bench/lds_probe.hip).  For k = 2..8, k x (CUs) workgroups of 128
+    threads each wait 200 us; their LDS size is swept across 163,840 / k in
+    steps of 64 bytes.  The kernel takes one wait while k fit on a CU and about
+    two once they do not.  Reports, per k, the largest size that still ran in
+    one wait, the smallest that took two, and the granule (the spacing of the
+    steps) the thresholds imply.  Then, for one-wavefront (64-thread)
+    workgroups at a few LDS sizes, the largest k that runs in one wait.  One
+    JSON line."""
+    import ctypes
+
+    import torch
+
+    lib = _probe_library()
+    lib.gdn_lds_residency_probe.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
+                                            ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64]
+    lib.gdn_lds_residency_probe.restype = ctypes.c_int32
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    stream = torch.cuda.current_stream()
+    wait_us = wait_ticks / 100.0  # the real-time counter runs at 100 MHz
+    result = {"metric": "workgroups resident per CU against LDS bytes", "cus": cus,
+              "wait_us": wait_us, "k": {}}
+
+    def rounds_at(k, lds, threads=128):
+        sink = torch.empty(k * cus, dtype=torch.int32, device="cuda:0")
+        times = []
+        for _ in range(repeats):
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            status = lib.gdn_lds_residency_probe(stream.cuda_stream, sink.data_ptr(), k * cus,
+                                                 threads, lds, wait_ticks)
+            stop.record(stream)
+            if status != 0:
+                raise RuntimeError(f"lds residency probe status {status} at {lds} bytes")
+            torch.cuda.synchronize()
+            times.append(start.elapsed_time(stop) * 1e3)
+        return sorted(times)[repeats // 2] / wait_us
+
+    for k in range(2, 9):
+        centre = 163840 // k
+        sizes = list(range(centre - 3072 - centre % 64, centre + 512, 64))
+        ratios = {lds: rounds_at(k, lds) for lds in sizes}
+        one = [lds for lds, r in ratios.items() if r < 1.5]
+        two = [lds for lds, r in ratios.items() if r >= 1.5]
+        entry = {"largest_in_one_wait": max(one) if one else None,
+                 "smallest_in_two_waits": min(two) if two else None,
+                 "rounds": {str(lds): round(r, 3) for lds, r in ratios.items()}}
+        if one and two:
+            # The allocation is ceil(lds / G) * G, and k of them fit in 163,840
+            # bytes: the largest fitting size is floor(163840 / k / G) * G.
+            entry["granules_consistent_with"] = [
+                g for g in (256, 512, 768, 1024, 1280, 1536, 2048)
+                if max(one) <= (163840 // k // g) * g < min(two)]
+        result["k"][str(k)] = entry
+        _log(f"lds residency k={k}: one wait up to {entry['largest_in_one_wait']}, "
+             f"two from {entry['smallest_in_two_waits']}")
+    result["one_wavefront"] = {}
+    for lds in (512, 5120, 5184, 6400, 6656, 7168):
+        ratios = {k: rounds_at(k, lds, threads=64) for k in range(8, 35)}
+        resident = max((k for k, r in ratios.items() if r < 1.5), default=None)
+        result["one_wavefront"][str(lds)] = {
+            "resident": resident, "rounds": {str(k): round(r, 3) for k, r in ratios.items()}}
+        _log(f"lds residency, 64-thread workgroups of {lds} B: {resident} per CU")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def placement_pass(buffers: int = 4, rounds: int = 2) -> int:
     """The config-2 dequantize into `buffers` separately allocated 16 GB output
     buffers, from two 4 GB code buffers, with each output buffer's own plain
@@ -2099,6 +2167,8 @@ def main() -> int:
                         help="the --profile launches of the config-2 codec and the probes only")
     parser.add_argument("--placement", action="store_true",
                         help="the config-2 dequantize and HBM probes on several output buffers")
+    parser.add_argument("--lds-residency", action="store_true",
+                        help="workgroups resident per CU against their LDS size")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every head "
@@ -2116,6 +2186,8 @@ def main() -> int:
         return profile_pass(codec_only=args.profile_codec)
     if args.placement:
         return placement_pass()
+    if args.lds_residency:
+        return lds_residency_pass()
     box = {"before": _box_info()}
     state, codes, smoothing, scales, dense, enc_ms, dec_ms, wall_ms = bench_codec(
         args.steps, args.warmup)

@@ -78,6 +78,7 @@ struct FitShared {
   float right[kDim];
   float total;          // the singular value's running sum
 };
+static_assert(workgroups_by_lds(sizeof(FitShared)) >= 4, "four heads per CU");
 
 struct Float16 {
   float v[16];

@@ -35,6 +35,16 @@ constexpr uint32_t kDtypeBF16 = 1;
 // Largest grid the launchers issue along x (hardware limit 2^31 - 1).
 constexpr uint64_t kMaxGrid = 0x7FFFFFFFull;
 
+// A CU has 163,840 bytes of LDS, and gfx950 allocates a workgroup's LDS in
+// 1,280-byte granules (measured: csrc/bench/lds_probe.hip), so k workgroups
+// share a CU only while k x ceil(bytes / 1280) x 1280 <= 163,840.  One byte
+// past a multiple of 1,280 costs a whole granule.
+constexpr uint32_t kLdsPerCu = 163840;
+constexpr uint32_t kLdsGranule = 1280;
+constexpr uint32_t workgroups_by_lds(uint64_t bytes) {
+  return kLdsPerCu / static_cast<uint32_t>((bytes + kLdsGranule - 1) / kLdsGranule * kLdsGranule);
+}
+
 // Every device pointer an entry point takes must be 16-byte aligned.  The
 // kernels move codes and fp32 tiles as 16-byte vectors and narrower words at
 // offsets that are multiples of their own width, so a 16-byte aligned base

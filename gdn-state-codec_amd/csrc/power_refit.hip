@@ -73,7 +73,7 @@ struct PowerArgs {
 
 // Compensators and records are fp16 values (the fitted ranks are rounded to
 // fp16 when formed), so they are kept as fp16 bits and widened exactly when
-// read: 32,424 bytes, five workgroups per CU.
+// read: 31,408 bytes, five workgroups per CU.
 struct PowerShared {
   int8_t code[kDim * kCodeStride];  // [value column][key row]
   alignas(8) uint16_t ck[kDim * kRank];
@@ -96,9 +96,8 @@ struct PowerShared {
   float record_suffix[kWindow];
   float scalar;  // norm inverse / singular value broadcast
   int flag;
-  float code_value[256];  // code / 127 by the code's byte pattern
 };
-static_assert(sizeof(PowerShared) <= 163840 / 5, "five workgroups per CU");
+static_assert(workgroups_by_lds(sizeof(PowerShared)) >= 5, "five workgroups per CU");
 
 // window_boundary.cpp:17-23.
 __device__ __forceinline__ float newton_sqrt(float value) {
@@ -110,22 +109,9 @@ __device__ __forceinline__ float newton_sqrt(float value) {
 
 __device__ __forceinline__ float h2f(uint16_t h) { return half_bits_to_float(h); }
 
-// code / 127 for an int8 code: IEEE division by 127 through its correctly
-// rounded reciprocal (div_by_reciprocal is exact for every numerator in
-// [2^-100, 2^120] and for +0, which covers the integers -127..127).
-__device__ __forceinline__ float code_over_127(int8_t code) {
-  return div_by_reciprocal(static_cast<float>(code), kQuantizedMaximum, kInvQuantizedMaximum);
-}
-// code / 127 from the workgroup's table: one LDS read instead of the four
-// instructions of the exact division.
-__device__ __forceinline__ float code_value(const PowerShared& sh, int8_t code) {
-  return sh.code_value[static_cast<uint8_t>(code)];
-}
-
-// The same value by arithmetic, div_by_127 of the code (the two-part division,
-// exact for every integer in [-128, 127]): in the operator's sums it replaces
-// a second LDS read, whose address depends on the first, with two VALU
-// instructions.
+// code / 127 by the two-part division (div_by_127, exact for every integer in
+// [-128, 127]): two VALU instructions, where a table of the 256 quotients
+// would cost a second LDS read whose address depends on the first.
 __device__ __forceinline__ float code_value_arith(int8_t code) {
   return div_by_127(static_cast<float>(code));
 }
@@ -226,7 +212,7 @@ __device__ void apply_transpose(PowerShared& sh, const float* vector, float* out
 // The re-encode of R minus the fit, for the 128 threads of a workgroup whose
 // LDS holds the state (codes [value column][key row] at kCodeStride, the old
 // and fitted compensators ck / cv / nk / nv [dim][rank], the records rk / rc
-// [dim][record], smoothing, scales, record suffixes and the code / 127 table):
+// [dim][record], smoothing, scales and record suffixes):
 // thread t owns key row t, whose 128 fitted cells stay in registers through
 // the smoothing, scale and code passes.  Writes the fitted residual to
 // workspace [key row][value column], next_smoothing[key], next_scales[value],
@@ -441,8 +427,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   }
   sh.smoothing[t] = (a.smoothing + vb)[t];
   sh.scales[t] = (a.scales + vb)[t];
-  sh.code_value[t] = code_over_127(static_cast<int8_t>(t));
-  sh.code_value[t + kThreads] = code_over_127(static_cast<int8_t>(t + kThreads));
   // BuildSuffix (:102-111), computed identically by every thread.
   float bs = 1.0f;
   for (int j = kWindow - 1; j >= 0; --j) {
@@ -572,8 +556,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   }
   sh.smoothing[t] = (a.smoothing + vb)[t];
   sh.scales[t] = (a.scales + vb)[t];
-  sh.code_value[t] = code_over_127(static_cast<int8_t>(t));
-  sh.code_value[t + kThreads] = code_over_127(static_cast<int8_t>(t + kThreads));
   // The suffix products (:106-111), computed identically by every thread.
   float bs = 1.0f;
   for (int j = kWindow - 1; j >= 0; --j) {
