@@ -18,7 +18,8 @@
 // One 64-lane wavefront per state.  The 24 coefficient sums are sequential
 // fp32 sums in the reference's order, one per lane (lanes 0..3 the old ranks,
 // 4..7 the fitted ones, 8..23 the records), over the input vector and the
-// input-side bases staged in LDS; the coefficients are then broadcast through
+// input-side bases staged in LDS (records first, then the rank bases in the
+// same area); the coefficients are then broadcast through
 // scalar registers and every lane evaluates two rows.  The squared norm is the
 // reference's sequential sum, evaluated identically by every lane from LDS.
 // Operations and their order are the reference's, so results are
@@ -69,13 +70,26 @@ __device__ __forceinline__ float readlane(float value, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), lane));
 }
 
+// LDS: x as fp16 bits and one 4 KiB staging area, 4,352 bytes in all.  The
+// CU allocates LDS in 1,280-byte granules, so that is four granules and 32
+// of these one-wavefront workgroups fit on a CU, where the wave slots allow
+// 32; six granules (the bases and the records staged side by side) allowed 21.
+struct RowsShared {
+  uint16_t x[kDim];
+  union {
+    __align__(16) uint16_t records[kWindow * kDim];  // [record][dim]
+    struct {
+      __align__(16) uint16_t old_in[kDim * kRank];  // [dim][rank]
+      __align__(16) uint16_t new_in[kRank * kDim];  // [rank][dim]
+    } ranks;
+    float values[kDim];  // finish: the rows, for the squared norm
+  };
+};
+static_assert(workgroups_by_lds(sizeof(RowsShared)) == 32, "32 one-wavefront workgroups per CU");
+
 template <bool kCommit>
 __global__ __launch_bounds__(kLanes) void encoded_rows_kernel(RankArgs a) {
-  __shared__ float x[kDim];
-  __shared__ __align__(16) uint16_t old_in[kDim * kRank];
-  __shared__ __align__(16) uint16_t new_in[kRank * kDim];
-  __shared__ __align__(16) uint16_t record_in[kWindow * kDim];
-  __shared__ float values[kDim];
+  __shared__ RowsShared sh;
 
   const int lane = threadIdx.x;
   const uint64_t state = blockIdx.x;
@@ -90,36 +104,46 @@ __global__ __launch_bounds__(kLanes) void encoded_rows_kernel(RankArgs a) {
   const float* const axis = (left_in ? a.scales : a.smoothing) + state * kDim;
   const uint16_t* const input = a.input + state * kDim * kVectorColumns;
 
-  // ---- stage x and the input-side bases ------------------------------------
-  for (int row = lane; row < kDim; row += kLanes) x[row] = half_bits_to_float(input[row * kVectorColumns]);
-  reinterpret_cast<uint4*>(old_in)[lane] =
+  // ---- stage x and the input-side records; the rank bases wait in registers
+  for (int row = lane; row < kDim; row += kLanes) sh.x[row] = input[row * kVectorColumns];
+  const uint4 old_words =
       reinterpret_cast<const uint4*>((left_in ? a.old_left : a.old_right) + basis)[lane];
-  reinterpret_cast<uint4*>(new_in)[lane] =
+  const uint4 new_words =
       reinterpret_cast<const uint4*>((left_in ? a.new_left : a.new_right) + basis)[lane];
   const uint4* const record_src =
       reinterpret_cast<const uint4*>((left_in ? a.record_left : a.record_right) + records);
 #pragma unroll
   for (int i = 0; i < kWindow * kDim / 8 / kLanes; ++i) {
-    reinterpret_cast<uint4*>(record_in)[i * kLanes + lane] = record_src[i * kLanes + lane];
+    reinterpret_cast<uint4*>(sh.records)[i * kLanes + lane] = record_src[i * kLanes + lane];
   }
   wave_lds_sync();
 
   // ---- PrepareState (:82-123): one sequential sum per coefficient lane ------
-  float coefficient = 0.0f;
-  if (lane < kCoefficients) {
-    const uint16_t* basis_lds;
-    int stride;
-    if (lane < kRank) {
-      basis_lds = old_in + lane;
-      stride = kRank;
-    } else if (lane < 2 * kRank) {
-      basis_lds = new_in + (lane - kRank) * kDim;
-      stride = 1;
-    } else {
-      basis_lds = record_in + (lane - 2 * kRank) * kDim;
-      stride = 1;
+  // Lanes 8..23 sum the records first; the rank bases then replace the
+  // records in the staging area and lanes 0..7 sum them.  Each term is an
+  // fp16 basis value times an fp16 input value, a product exact in fp32, so
+  // `total += b * x` rounds exactly what fma(b, x, total) rounds: one
+  // v_fma_mix_f32 per term, widening both halves itself.
+  const auto sum = [&](const uint16_t* basis_lds, int stride) {
+    float total = 0.0f;
+    for (int i = 0; i < kDim; ++i) {
+      total = __builtin_fmaf(half_bits_to_float(basis_lds[i * stride]),
+                             half_bits_to_float(sh.x[i]), total);
     }
-    for (int i = 0; i < kDim; ++i) coefficient += half_bits_to_float(basis_lds[i * stride]) * x[i];
+    return total;
+  };
+  float coefficient = 0.0f;
+  if (lane >= 2 * kRank && lane < kCoefficients) {
+    coefficient = sum(sh.records + (lane - 2 * kRank) * kDim, 1);
+  }
+  wave_lds_sync();
+  reinterpret_cast<uint4*>(sh.ranks.old_in)[lane] = old_words;
+  reinterpret_cast<uint4*>(sh.ranks.new_in)[lane] = new_words;
+  wave_lds_sync();
+  if (lane < kRank) {
+    coefficient = sum(sh.ranks.old_in + lane, kRank);
+  } else if (lane < 2 * kRank) {
+    coefficient = sum(sh.ranks.new_in + (lane - kRank) * kDim, 1);
   }
   // Record coefficients times their suffixes, and the whole window's product.
   const float* const decay = a.record_decay + state * kWindow;
@@ -173,11 +197,11 @@ __global__ __launch_bounds__(kLanes) void encoded_rows_kernel(RankArgs a) {
   } else {
     // Squared norm: the reference's sequential sum over the rows, evaluated
     // identically in every lane from LDS.
-    values[lane] = row_value[0];
-    values[lane + kLanes] = row_value[1];
+    sh.values[lane] = row_value[0];
+    sh.values[lane + kLanes] = row_value[1];
     wave_lds_sync();
     float squared_norm = 0.0f;
-    for (int row = 0; row < kDim; ++row) squared_norm += values[row] * values[row];
+    for (int row = 0; row < kDim; ++row) squared_norm += sh.values[row] * sh.values[row];
     const float inverse = squared_norm > 1.0e-20f ? 1.0f / newton_sqrt(squared_norm) : 0.0f;
     uint16_t* const output = a.output + state * kDim * kVectorColumns;
 #pragma unroll
