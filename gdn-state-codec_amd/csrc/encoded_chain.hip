@@ -76,8 +76,7 @@ struct ChainShared {
   uint16_t basis[2][kCoefficientRows][kBasisStride];
   float axis[2][kDim];
   float decay[kWindow];
-  uint16_t vector[kDim];  // the current vector, fp16 bits
-  __attribute__((aligned(16))) float x[kDim];  // fp16(vector) widened
+  __attribute__((aligned(16))) uint16_t vector[kDim];  // the current vector, fp16 bits
   __attribute__((aligned(16))) uint32_t q[kDim / 4];  // the quantized vector
   int32_t p[kDim];        // the projection
   __attribute__((aligned(16))) float values[kDim];  // the rows' values, for the norm
@@ -127,20 +126,24 @@ __device__ void chain_prepare(ChainShared& sh, int side, int lane) {
 __device__ void chain_rows(ChainShared& sh, int in_side, uint32_t ranks, int lane,
                            float (&row_value)[2]) {
   const int out_side = 1 - in_side;
-  // The sequential coefficient sums, one per lane 0..23, over x.
-  sh.x[lane] = half_bits_to_float(sh.vector[lane]);
-  sh.x[lane + kChainLanes] = half_bits_to_float(sh.vector[lane + kChainLanes]);
-  wave_lds_sync();
+  // The sequential coefficient sums, one per lane 0..23, over the vector.
+  // Each term is an fp16 basis value times an fp16 vector value, a product
+  // exact in fp32, so `coefficient += b * x` rounds exactly what
+  // fma(b, x, coefficient) rounds: one v_fma_mix_f32 per term, reading both
+  // halves of the packed words itself.
   float coefficient = 0.0f;
   if (lane < kCoefficientRows) {
     const uint16_t* const basis = sh.basis[in_side][lane];
+    const auto term = [](uint32_t b, uint32_t x, float total) {
+      return __builtin_fmaf(half_bits_to_float(b), half_bits_to_float(x), total);
+    };
     for (int i = 0; i < kDim; i += 4) {
       const uint2 b = *reinterpret_cast<const uint2*>(basis + i);
-      const float4 xv = *reinterpret_cast<const float4*>(sh.x + i);
-      coefficient += half_bits_to_float(b.x & 0xFFFFu) * xv.x;
-      coefficient += half_bits_to_float(b.x >> 16) * xv.y;
-      coefficient += half_bits_to_float(b.y & 0xFFFFu) * xv.z;
-      coefficient += half_bits_to_float(b.y >> 16) * xv.w;
+      const uint2 x = *reinterpret_cast<const uint2*>(sh.vector + i);
+      coefficient = term(b.x, x.x, coefficient);
+      coefficient = term(b.x >> 16, x.x >> 16, coefficient);
+      coefficient = term(b.y, x.y, coefficient);
+      coefficient = term(b.y >> 16, x.y >> 16, coefficient);
     }
   }
   // Record coefficients times their suffixes, and the whole window's product.
