@@ -17,10 +17,10 @@
 // the CPU statement of the reference kernel.  One 128-thread workgroup per
 // state, operands staged in LDS: the codes at a 132-byte row stride so both
 // the row walk and the column walk are free of bank conflicts, compensators
-// and records as fp16 bits, and a 256-entry table of code / 127.  The fitted
-// residual is evaluated once per cell, one key row per thread held in
-// registers for the smoothing, scale and code passes, and written once to the
-// workspace.
+// and records as fp16 bits (31,408 bytes: 25 of the CU's 1,280-byte LDS
+// granules, five workgroups per CU).  The fitted residual is evaluated once
+// per cell, one key row per thread held in registers for the smoothing, scale
+// and code passes, and written once to the workspace.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
