@@ -174,9 +174,18 @@ __global__ __launch_bounds__(kSvdThreads) void exact_svd_kernel(SvdArgs a) {
       if (active) {
         // Rotate (x, y) -> (c x - s y, s x + c y) by the angle of magnitude
         // at most pi/4 that makes the rows orthogonal: t = s/c solves
-        // t^2 + 2 zeta t - 1 = 0 with zeta = (beta - alpha) / (2 gamma).
-        const double zeta = (beta - alpha) / (2.0 * gamma);
-        const double tangent = copysign(1.0, zeta) / (fabs(zeta) + sqrt(fma(zeta, zeta, 1.0)));
+        // t^2 + 2 zeta t - 1 = 0 with zeta = (beta - alpha) / (2 gamma), and
+        // the smaller root sign(zeta) / (|zeta| + sqrt(1 + zeta^2)), times
+        // |2 gamma| above and below, is 2 gamma sign(d) / (|d| + sqrt(d^2 +
+        // 4 gamma^2)) with d = beta - alpha: one dependent division fewer.
+        // After the head's scaling alpha, beta <= 128 and gamma^2 > 2^-264, so
+        // neither square overflows or underflows.
+        const double d = beta - alpha;
+        const double two_gamma = 2.0 * gamma;
+        // sign(zeta) |2 gamma| = 2 gamma sign(d), with sign(+0) = +1 (for
+        // d = 0, zeta = +0 / (2 gamma) carries the sign of gamma).
+        const double tangent = (d < 0.0 ? -two_gamma : two_gamma) /
+                               (fabs(d) + sqrt(fma(d, d, two_gamma * two_gamma)));
         const double c = 1.0 / sqrt(fma(tangent, tangent, 1.0));
         const double s = c * tangent;
 #pragma unroll
